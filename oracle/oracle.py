@@ -1,0 +1,317 @@
+"""CPU oracle for the EXL3 routed-expert path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg may import this module, and only as the checker: the product package never
+imports it and fails loudly when its HIP library is missing.
+
+Contents (each function cites the reference file:line it restates; paths are
+relative to the vllm-exl3 repository root):
+
+* bit-exact trellis decode and dequant via ``liboracle.so`` (C, built by
+  ``make -C oracle``) -- ``csrc/exl3_dequant.cuh``, ``csrc/bindings.cpp:15-100``;
+* dequant + fp32 matmul GEMV -- ``csrc/bindings.cpp:134-147``;
+* the per-expert MoE loop -- ``src/vllm_exl3/exl3.py:2357-2413`` with the
+  rounding points of ``tests/test_native_moe_contract.py:100-115``;
+* routing helpers -- ``exl3.py:2332-2354``;
+* the int4-asymmetric paged KV cache (a format this build defines; the
+  reference's own KV format is NVFP4) and dense softmax attention.
+
+Parity status of every function is listed in ``ORACLE_PINS`` below.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import numpy as np
+
+_HERE = pathlib.Path(__file__).resolve().parent
+
+# How each oracle function is pinned (a function without a check would read
+# "parity unpinned").
+ORACLE_PINS = {
+    "f16<->f32": "reference golden vectors tests/test_dequant_parity.py:18-81, "
+                 "numpy float16 casts over all 65536 patterns, oracle/_ref harness",
+    "decode_codebook": "golden vectors tests/test_dequant_parity.py:84-104 (MCG, mul1); "
+                       "all 65536 windows x 3 codebooks vs oracle/_ref (incl. 3INST)",
+    "read_window": "every bit position of K=2,3,4,8 tiles vs oracle/_ref; brute-force bit list",
+    "tile_position": "bijection + literal swizzle loop of csrc/bindings.cpp:51-75",
+    "hadamard": "vs oracle/_ref (bit-exact); H.H = 128 I; float64 matrix form",
+    "dequant": "composition: float64 diag(suh) H Wq H diag(svh)/128 within one fp16 ulp; "
+               "suh=svh=1 round trip; constant tile gives one non-zero per block",
+    "moe_loop": "reference activation vectors tests/test_activation_parity.py:46-53; "
+                "single-expert reduction to gemv; routing exact-sum stub",
+    "kv_int4": "closed form + brute force on tiny pages (format defined in-repo)",
+    "attention": "float64 textbook softmax attention; uniform-key closed form",
+}
+
+
+def _load_lib() -> ctypes.CDLL:
+    path = _HERE / "liboracle.so"
+    if not path.exists():
+        raise RuntimeError(f"oracle library missing: run `make -C {_HERE}` ({path})")
+    lib = ctypes.CDLL(str(path))
+    u16, i32, f32 = ctypes.c_uint16, ctypes.c_int, ctypes.c_float
+    p = ctypes.c_void_p
+    lib.oc_f16_to_f32.restype = f32
+    lib.oc_f16_to_f32.argtypes = [u16]
+    lib.oc_f32_to_f16.restype = u16
+    lib.oc_f32_to_f16.argtypes = [f32]
+    lib.oc_decode_codebook.restype = u16
+    lib.oc_decode_codebook.argtypes = [u16, i32]
+    lib.oc_read_window.restype = u16
+    lib.oc_read_window.argtypes = [p, i32, ctypes.c_uint32]
+    lib.oc_decode_index.restype = u16
+    lib.oc_decode_index.argtypes = [p, i32, i32, i32]
+    lib.oc_tile_position.restype = None
+    lib.oc_tile_position.argtypes = [i32, ctypes.POINTER(i32), ctypes.POINTER(i32)]
+    lib.oc_tile_position_loop.restype = None
+    lib.oc_tile_position_loop.argtypes = [p, p]
+    lib.oc_hadamard.restype = None
+    lib.oc_hadamard.argtypes = [p, i32]
+    lib.oc_decode_tiles.restype = None
+    lib.oc_decode_tiles.argtypes = [p, i32, i32, i32, i32, p]
+    lib.oc_dequant.restype = None
+    lib.oc_dequant.argtypes = [p, i32, i32, i32, i32, p, p, p]
+    return lib
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        _LIB = _load_lib()
+    return _LIB
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+CODEBOOKS = {"3inst": 0, "mcg": 1, "mul1": 2}
+
+
+# ---------------------------------------------------------------------------
+# Trellis decode
+# ---------------------------------------------------------------------------
+
+def decode_codebook(window: int, cb: int) -> int:
+    """fp16 bits of one window.  csrc/exl3_dequant.cuh:105-124."""
+    return int(lib().oc_decode_codebook(window & 0xFFFF, cb))
+
+
+def decode_codebook_table(cb: int) -> np.ndarray:
+    """All 65536 windows -> fp16 bit patterns (uint16)."""
+    L = lib()
+    return np.array([L.oc_decode_codebook(w, cb) for w in range(65536)], dtype=np.uint16)
+
+
+def read_window(tile_u16: np.ndarray, K: int, bit: int) -> int:
+    """csrc/exl3_dequant.cuh:141-159 (circular MSB-first 16-bit window)."""
+    t = np.ascontiguousarray(tile_u16, dtype=np.uint16)
+    return int(lib().oc_read_window(_ptr(t), K, bit))
+
+
+def tile_positions() -> tuple[np.ndarray, np.ndarray]:
+    """(row, col) of each of the 256 tile indices.  csrc/bindings.cpp:37-77."""
+    rows = np.zeros(256, dtype=np.int32)
+    cols = np.zeros(256, dtype=np.int32)
+    L = lib()
+    r, c = ctypes.c_int(), ctypes.c_int()
+    for i in range(256):
+        L.oc_tile_position(i, ctypes.byref(r), ctypes.byref(c))
+        rows[i], cols[i] = r.value, c.value
+    return rows, cols
+
+
+def tile_positions_loop() -> tuple[np.ndarray, np.ndarray]:
+    rows = np.zeros(256, dtype=np.int32)
+    cols = np.zeros(256, dtype=np.int32)
+    lib().oc_tile_position_loop(_ptr(rows), _ptr(cols))
+    return rows, cols
+
+
+def hadamard_f32(v: np.ndarray) -> np.ndarray:
+    """Unnormalised fp32 butterfly.  csrc/exl3_dequant.cuh:168-179."""
+    out = np.ascontiguousarray(v, dtype=np.float32).copy()
+    lib().oc_hadamard(_ptr(out), out.size)
+    return out
+
+
+def decode_tiles(trellis: np.ndarray, K: int, cb: int) -> np.ndarray:
+    """Codebook values at swizzled positions, no rotation: fp32 [in, out]."""
+    t = np.ascontiguousarray(trellis, dtype=np.int16)
+    tk, tn, w = t.shape
+    assert w == 16 * K
+    out = np.empty((tk * 16, tn * 16), dtype=np.float32)
+    lib().oc_decode_tiles(_ptr(t), tk, tn, K, cb, _ptr(out))
+    return out
+
+
+def dequant(trellis: np.ndarray, suh: np.ndarray, svh: np.ndarray, K: int, cb: int) -> np.ndarray:
+    """Bit-exact fp16 W[in, out].  csrc/bindings.cpp:15-100 (+ cb 0 for 3INST)."""
+    t = np.ascontiguousarray(trellis, dtype=np.int16)
+    tk, tn, w = t.shape
+    if w != 16 * K:
+        raise ValueError("trellis last dimension must be 16*K")
+    if (tk * 16) % 128 or (tn * 16) % 128:
+        raise ValueError("trellis dimensions must reconstruct whole 128-element Hadamard blocks")
+    su = np.ascontiguousarray(suh, dtype=np.float16).view(np.uint16)
+    sv = np.ascontiguousarray(svh, dtype=np.float16).view(np.uint16)
+    out = np.empty((tk * 16, tn * 16), dtype=np.uint16)
+    lib().oc_dequant(_ptr(t), tk, tn, K, cb, _ptr(su), _ptr(sv), _ptr(out))
+    return out.view(np.float16)
+
+
+# ---------------------------------------------------------------------------
+# Hadamard helpers (float64 closed forms used by the tests)
+# ---------------------------------------------------------------------------
+
+def hadamard_matrix(n: int = 128) -> np.ndarray:
+    """Sylvester Walsh-Hadamard matrix (natural order), entries +-1."""
+    h = np.array([[1.0]])
+    while h.shape[0] < n:
+        h = np.block([[h, h], [h, -h]])
+    return h
+
+
+def block_hadamard(x: np.ndarray, axis: int = -1) -> np.ndarray:
+    """Normalised 128-block Hadamard along ``axis`` in float64."""
+    x = np.moveaxis(np.asarray(x, dtype=np.float64), axis, -1)
+    n = x.shape[-1]
+    assert n % 128 == 0
+    h = hadamard_matrix(128) / np.sqrt(128.0)
+    y = (x.reshape(*x.shape[:-1], n // 128, 128) @ h).reshape(x.shape)
+    return np.moveaxis(y, -1, axis)
+
+
+# ---------------------------------------------------------------------------
+# GEMV / MoE (reference eager semantics)
+# ---------------------------------------------------------------------------
+
+def gemv(x: np.ndarray, w16: np.ndarray) -> np.ndarray:
+    """y = fp16(x) @ W in fp32.  csrc/bindings.cpp:144-146 (x cast to fp16 at
+    the plugin boundary, exl3.py:2856)."""
+    xf = np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    return xf @ np.asarray(w16, dtype=np.float32)
+
+
+def map_topk_to_local(ids: np.ndarray, n_local: int) -> np.ndarray:
+    """Invalid ids -> n_local sentinel.  exl3.py:2330-2341 (no expert map)."""
+    ids = np.asarray(ids, dtype=np.int64)
+    return np.where((ids < 0) | (ids >= n_local), n_local, ids)
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32)
+    return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+
+def moe_reference(x: np.ndarray, ids: np.ndarray, weights: np.ndarray,
+                  experts: list[dict], limit: float | None = None,
+                  act: str = "silu", round_down: bool = False) -> np.ndarray:
+    """Per-expert eager loop, fp32 accumulation.
+
+    ``experts[e]`` holds dense fp16 matrices ``gate`` [H, I] (or None for a
+    gateless layer), ``up`` [H, I], ``down`` [I, H] as produced by
+    ``dequant``.  Rounding points follow exl3.py:2357-2413 and
+    tests/test_native_moe_contract.py:100-115: g and u rounded to fp16,
+    clamp (gate from above, up symmetric), act in fp32, act -> fp16, down in
+    fp32 (optionally rounded to fp16), weighted fp32 sum over the token's
+    routes in slot order.  Non-local ids (>= len(experts)) are skipped.
+    """
+    x = np.asarray(x)
+    T, H = x.shape
+    ids = map_topk_to_local(ids, len(experts))
+    out = np.zeros((T, H), dtype=np.float32)
+    xh = np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    for t in range(T):
+        for k in range(ids.shape[1]):
+            e = int(ids[t, k])
+            if e >= len(experts):
+                continue
+            pack = experts[e]
+            xv = xh[t:t + 1]
+            u = (xv @ pack["up"].astype(np.float32)).astype(np.float16).astype(np.float32)
+            if pack.get("gate") is None:
+                if limit is not None and limit > 0:
+                    u = np.clip(u, -limit, limit)
+                a = np.square(np.maximum(u, 0))
+            else:
+                g = (xv @ pack["gate"].astype(np.float32)).astype(np.float16).astype(np.float32)
+                if limit is not None and limit > 0:
+                    g = np.minimum(g, np.float32(limit))
+                    u = np.clip(u, -limit, limit)
+                if act == "swiglu_oai":
+                    a = (u + 1.0) * g * (1.0 / (1.0 + np.exp(-1.702 * g)))
+                else:
+                    a = silu(g) * u
+            a = a.astype(np.float32).astype(np.float16).astype(np.float32)
+            d = a @ pack["down"].astype(np.float32)
+            if round_down:
+                d = d.astype(np.float16).astype(np.float32)
+            out[t] += np.float32(weights[t, k]) * d[0]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# int4-asymmetric paged KV cache (format defined in this build)
+# ---------------------------------------------------------------------------
+
+KV_GROUP = 32
+
+
+def kv_quantize_rows(x: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Quantise [..., D] rows per 32-element group.
+
+    zero = fp16(min), scale = fp16((max - min) / 15) computed in fp32;
+    q = clamp(rint((x - zero) / scale), 0, 15) in fp32 with the fp16-rounded
+    zero and scale (scale 0 -> q 0).  Returns (q uint8 [..., D], scale fp16
+    [..., D/32], zero fp16 [..., D/32]).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    D = x.shape[-1]
+    g = x.reshape(*x.shape[:-1], D // KV_GROUP, KV_GROUP)
+    mn = g.min(axis=-1)
+    mx = g.max(axis=-1)
+    zero = mn.astype(np.float16)
+    scale = ((mx - mn) / np.float32(15.0)).astype(np.float32).astype(np.float16)
+    zf = zero.astype(np.float32)[..., None]
+    sf = scale.astype(np.float32)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(sf > 0, np.rint((g - zf) / np.where(sf > 0, sf, 1)), 0)
+    q = np.clip(q, 0, 15).astype(np.uint8).reshape(x.shape)
+    return q, scale, zero
+
+
+def kv_dequantize_rows(q: np.ndarray, scale: np.ndarray, zero: np.ndarray) -> np.ndarray:
+    """x = q * scale + zero in fp32 (fp16 scale/zero widened exactly)."""
+    D = q.shape[-1]
+    qg = q.reshape(*q.shape[:-1], D // KV_GROUP, KV_GROUP).astype(np.float32)
+    v = qg * scale.astype(np.float32)[..., None] + zero.astype(np.float32)[..., None]
+    return v.reshape(q.shape).astype(np.float32)
+
+
+def attention_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """Dense softmax attention for one decode step, float64.
+
+    q [B, Hq, D]; k, v [B, Hkv, L, D]; GQA with Hq/Hkv query heads per KV head.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    B, Hq, D = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    qg = q.reshape(B, Hkv, g, D)
+    s = np.einsum("bhgd,bhld->bhgl", qg, k) * scale
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    o = np.einsum("bhgl,bhld->bhgd", p, v)
+    return o.reshape(B, Hq, D)
