@@ -6,10 +6,10 @@
  * (hipStream_t passed as void*; NULL = the default stream), launches
  * asynchronously on that stream, never synchronises and never allocates.
  * Scratch memory is passed in by the caller as a workspace whose size is
- * returned by the matching *_workspace_size() query; the workspace must be
- * zero-filled once when first allocated (kernels leave their counters at zero
- * again when they finish), and calls that share one workspace must be
- * ordered on one stream.
+ * returned by the matching *_workspace_size() query; it needs no
+ * initialisation, and calls that share one workspace must be ordered on one
+ * stream.  No kernel waits on another workgroup: split-K partial sums are
+ * finished by the next kernel in stream order.
  *
  * Return value: 0 on success, a negative status on failure; the message is
  * available from exl3_last_error() (thread-local).  Validation failures
@@ -57,6 +57,54 @@ int exl3_dequant_trellis(const int16_t* trellis, int64_t tiles_k, int64_t tiles_
  * Replaces ExLlamaV3's `reconstruct` as called at src/vllm_exl3/exl3.py:3130-3156. */
 int exl3_decode_tiles(const int16_t* trellis, int64_t tiles_k, int64_t tiles_n, int64_t K,
                       int codebook, uint16_t* out_w, void* stream);
+
+
+/* ---------------------------------------------------------------------------
+ * Decode GEMV / GEMM (streams packed trellis, fused input and output
+ * rotations).  x is [m, in] (x_dtype 0 fp16, 1 bf16, 2 fp32; values are
+ * rounded to fp16 first, as the reference casts at its boundary), out is
+ * [m, out] of out_dtype.  K in {2,3,4}; any m >= 1 (rows are processed in
+ * groups of 16 with the weights streamed once per group).
+ * Replaces vllm_exl3_c.exl3_gemv (csrc/bindings.cpp:134-147,
+ * csrc/exl3_gemv.cu:23-63) and vllm_exl3_c.exl3_gemm (csrc/bindings.cpp:110-115,
+ * csrc/exl3_gemm.cu:8-31). */
+int64_t exl3_gemm_workspace_size(int64_t m, int64_t in_features, int64_t out_features);
+int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* trellis, int64_t tiles_k,
+              int64_t tiles_n, int64_t K, int codebook, const uint16_t* suh, const uint16_t* svh,
+              void* out, int out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Routed-expert MoE forward for T decode rows in one launch sequence:
+ * device-side routing sort -> fused gate/up GEMV + activation + down-input
+ * rotation -> down GEMV -> per-token combine in slot order (no atomics in
+ * the sum, bit-identical run to run).
+ *   tables: int64 device arrays of device addresses, one entry per local
+ *     expert (the reference's pointer tables, src/vllm_exl3/exl3.py:2475-2508);
+ *     gate tables may be NULL when gateless != 0.
+ *   k_gate/k_up/k_down: optional int8 per-expert K tables (NULL -> K_*).
+ *   ids: [T, topk] int32 (ids_dtype 0) or int64 (1); ids outside [0, n_local)
+ *     are non-local routes and contribute nothing.
+ *   weights: [T, topk] fp16/bf16/fp32 routing weights.
+ *   n_valid: optional device int32[1]; rows >= *n_valid are padding and
+ *     produce exact zeros (never read on the host).
+ *   act: 0 silu, 2 relu2 (gateless), 3 swiglu-oai; swiglu_limit 0 = no clamp.
+ *   out: [T, hidden] of out_dtype.
+ * Replaces vllm_exl3_c.p2b_fused_moe / p2b_fused_moe_mk / p2b_fused_moe_padded
+ * (csrc/bindings.cpp:158-195; csrc/p2b_moe.cu:643-1071, 1295-2487) and the
+ * decode rows of ExLlamaV3's exl3_moe / exl3_moe_mixedk
+ * (src/vllm_exl3/exl3.py:3491-3579). */
+int64_t exl3_moe_workspace_size(int64_t T, int64_t topk, int64_t n_local, int64_t hidden,
+                                int64_t inter, int gateless);
+int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hidden, int64_t inter,
+                     const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                     const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                     const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                     int64_t n_local, const int8_t* k_gate, const int8_t* k_up, const int8_t* k_down,
+                     int64_t K_gate, int64_t K_up, int64_t K_down, int codebook, int gateless,
+                     int act, float swiglu_limit, const void* ids, int ids_dtype,
+                     const void* weights, int w_dtype, int64_t topk, const int32_t* n_valid,
+                     void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+                     void* stream);
 
 #ifdef __cplusplus
 }

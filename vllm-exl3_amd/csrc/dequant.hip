@@ -185,6 +185,7 @@ EXL3_API int exl3_dequant_trellis(const int16_t* trellis, int64_t tiles_k, int64
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)dequant_kernel<2>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, cap);
+        if (e != hipSuccess) (void)hipGetLastError();
         return e;
     }();
     EXL3_HIP(attr_status);

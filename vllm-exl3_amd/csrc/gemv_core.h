@@ -1,0 +1,215 @@
+// Streaming EXL3 decode-GEMV core for gfx950 (small row counts: decode).
+//
+// One workgroup (4 wave64s) owns one 128-column block of one or two
+// projections over a K-split range of input rows, for every activation row of
+// one routing slot (or of the plain linear).  Per wave, per tile row (8 packed
+// 16x16 tiles = 256*K contiguous bytes):
+//   * one coalesced 128-bit global load per lane into registers, software
+//     pipelined kDepth rows ahead, then one ds_write_b128 into the wave's LDS
+//     slot (no workgroup barrier in the main loop);
+//   * each lane reads the two uint32 words that cover the windows of its four
+//     consecutive tile indices, funnel-shifts them once, and decodes four
+//     weights with bfe / mad_u32_u24 / pk_mad_u16 / bitop3;
+//   * the codebook's (lo, hi) half pair is fed to MFMA as-is: the K dimension
+//     is doubled (each activation duplicated), so the hardware sums the two
+//     halves in fp32 and no fp16 add, pack or permute is spent per weight;
+//   * one v_mfma_f32_16x16x32_f16 per tile accumulates 16 rows x 16 columns.
+// The MFMA row/column order inside a tile is a permutation of the reference's
+// tile layout chosen so that every lane's four weights are consecutive tile
+// indices (one word pair per lane per tile); activations are staged in LDS in
+// the matching permuted, duplicated order, and results are un-permuted when
+// they leave the accumulators.
+//
+// Split-K partials go to a workspace; the last workgroup of a column block
+// (an agent-scope counter that the finisher resets) sums them in split order
+// and runs the epilogue: output 128-Hadamard x svh, and for the MoE gate/up
+// phase the SwiGLU plus the down projection's input rotation.
+#pragma once
+
+#include "exl3_common.h"
+
+namespace exl3 {
+
+enum GemvMode : int { kModeLinear = 0, kModeGateUp = 1, kModeDown = 2 };
+// Activation ids follow the reference (src/vllm_exl3/exl3.py MOE_ACT_*):
+enum ActId : int { kActSilu = 0, kActRelu2 = 2, kActSwigluOai = 3 };
+enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kDepth = 4;          // tile rows in flight per wave
+constexpr int kStageBytes = 1024;  // one tile row of 8 tiles at K <= 4
+
+struct GemvParams {
+    // Activations.  Linear / GateUp: raw rows [*, in] of x_dtype, gathered by
+    // row_token; Down: rotated fp16 rows [route_rows, in].
+    const void* x;
+    int x_dtype;
+    int64_t x_stride;
+    // Weights.  Linear: direct pointers.  MoE: device pointer tables indexed
+    // by expert id (gate t/su/sv, up t/su/sv, down t/su/sv).
+    const int16_t* w_trellis;
+    const uint16_t* w_suh;
+    const uint16_t* w_svh;
+    const int64_t* tab[9];
+    const int8_t* ktab[3];  // per-expert K per projection (nullable)
+    int kuni[3];            // uniform K per projection (when ktab is null)
+    int gateless;
+    int in_features, out_features;
+    // Routing (MoE): filled on device by the route kernel.
+    const int* n_active;
+    const int* slot_expert;
+    const int* slot_start;
+    const int* slot_rows;
+    const int* row_token;
+    int max_slots;
+    int m_rows;  // linear: number of rows
+    // Output.  Linear: out_dtype rows [m, out]; GateUp: fp16 act_h rows
+    // [route_rows, inter] (already rotated for the down projection); Down:
+    // fp32 rows [route_rows, hidden].
+    void* out;
+    int out_dtype;
+    int64_t out_stride;
+    // Split-K: raw partial sums go to ws[q][s][row][out_features]; they are
+    // finished by the consumer kernel (the down kernel's activation staging,
+    // the combine kernel, or the linear finish kernel), so no workgroup ever
+    // waits on another and no device-scope fence is needed.
+    int S;         // splits of the input dimension
+    int R_hb;      // 128-row Hadamard blocks per split
+    int C_hb;      // Hadamard blocks whose activations are staged at once
+    int MRB;       // rows per row group (<= 16)
+    int n_rows_ws; // rows addressed in the workspace (route rows or m)
+    float* ws;
+    // Down mode: gate/up raw partials to finish while staging activations.
+    const float* src_ws;
+    int src_S;
+    float limit;
+    int act;
+};
+
+// ---------------------------------------------------------------------------
+// Lane geometry
+// ---------------------------------------------------------------------------
+// MFMA 16x16x32 f16 operands: lane l = nu + 16 g holds B'[8g..8g+7][nu] and
+// A'[m = l % 16][8g..8g+7]; D[4g + i][nu] comes back in component i.
+// Tile index bits b0..b7 map to (row, col) as row = b0|b3<<1|b4<<2|b1<<3,
+// col = b5|b6<<1|b7<<2|b2<<3.  Lane l decodes tile indices 4q(l)+i, i=0..3,
+// which land at MFMA row kappa = 4g + i (tile row pi(kappa)) and MFMA column
+// nu (tile column sigma(nu)).
+__device__ __forceinline__ int lane_q(int l) {
+    return (l & 1) | (((l >> 4) & 1) << 1) | (((l >> 5) & 1) << 2) | (((l >> 1) & 1) << 3) |
+           (((l >> 2) & 1) << 4) | (((l >> 3) & 1) << 5);
+}
+// MFMA k-row kappa (0..15) -> tile row.
+__device__ __forceinline__ int pi_row(int k) {
+    return (k & 1) | (((k >> 2) & 1) << 1) | (((k >> 3) & 1) << 2) | (((k >> 1) & 1) << 3);
+}
+// tile row -> MFMA k-row kappa (inverse of pi_row).
+__device__ __forceinline__ int pi_inv(int r) {
+    return (r & 1) | (((r >> 3) & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 3);
+}
+// MFMA column nu -> tile column.
+__device__ __forceinline__ int sigma_col(int n) { return (n >> 1) | ((n & 1) << 3); }
+
+struct LaneWords {
+    uint32_t off_hi;  // byte offset (in a tile) of the word holding the earlier bits
+    uint32_t off_lo;  // byte offset of the word holding the last bit
+    uint32_t shift;   // funnel shift that puts the last window at bit 0
+};
+
+template <int K>
+__device__ __forceinline__ LaneWords lane_words(int lane) {
+    constexpr int n32 = 8 * K;
+    const int q = lane_q(lane);
+    const int E = (4 * q + 4) * K;  // end (exclusive) of the lane's last window
+    const int wb = (E - 1) >> 5;
+    LaneWords w;
+    w.off_lo = 4u * wb;
+    w.off_hi = 4u * ((wb + n32 - 1) % n32);
+    w.shift = 32u * (wb + 1) - E;
+    return w;
+}
+
+// Decode the lane's four weights of one tile into MFMA B registers (each a
+// (lo, hi) fp16 pair whose sum is the weight).
+template <int K, int CB>
+__device__ __forceinline__ void decode4(uint32_t hi, uint32_t lo, uint32_t shift, uint32_t b[4]) {
+    const uint32_t s = __builtin_amdgcn_alignbit(hi, lo, shift);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = __builtin_amdgcn_ubfe(s, (3 - i) * K, 16);
+        if constexpr (CB == kCbMul1) {
+            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(w));  // (value, +0)
+        } else {
+            // x*C mod 2^32 = x*C_lo + (x*C_hi << 16): the low product on the
+            // full-rate 24-bit multiplier (the 3INST addend folded in), the
+            // high half with one packed 16-bit mad (lo lane adds 0).  Written
+            // as asm because the compiler otherwise re-fuses the pieces into a
+            // quarter-rate v_mul_lo_u32.
+            constexpr uint32_t C = (CB == kCb3Inst) ? 89226354u : 0xCBAC1FEDu;
+            constexpr uint32_t A = (CB == kCb3Inst) ? 64248484u : 0u;
+            const uint32_t c_lo = C & 0xFFFFu, c_hi = C & 0xFFFF0000u;
+            uint32_t lo_prod, x;
+            if constexpr (A != 0) {
+                asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(lo_prod) : "v"(w), "s"(c_lo), "v"(A));
+            } else {
+                asm("v_mul_u32_u24 %0, %1, %2" : "=v"(lo_prod) : "v"(w), "s"(c_lo));
+            }
+            asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel_hi:[0,1,1]" : "=v"(x) : "v"(w), "s"(c_hi), "v"(lo_prod));
+            b[i] = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+        }
+    }
+}
+
+__device__ __forceinline__ float4_t mfma16x16x32(const half8_t& a, const uint32_t b[4], float4_t c) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 bv = {b[0], b[1], b[2], b[3]};
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8_t, bv), c, 0, 0, 0);
+}
+
+// Butterfly over 128 values held as (lane, lane + 64), strides 1..64.
+__device__ __forceinline__ void had128(float& v0, float& v1, int lane) {
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        float p0 = __shfl_xor(v0, s, 64);
+        float p1 = __shfl_xor(v1, s, 64);
+        if (lane & s) {
+            v0 = p0 - v0;
+            v1 = p1 - v1;
+        } else {
+            v0 = v0 + p0;
+            v1 = v1 + p1;
+        }
+    }
+    float a = v0, b = v1;
+    v0 = a + b;
+    v1 = a - b;
+}
+
+__device__ __forceinline__ float load_act(const void* x, int dtype, int64_t idx) {
+    // The reference casts activations to fp16 at the boundary
+    // (src/vllm_exl3/exl3.py:2856); mirror that rounding for every dtype.
+    if (dtype == kF16) return (float)bits_to_half(reinterpret_cast<const uint16_t*>(x)[idx]);
+    float f;
+    if (dtype == kBF16) {
+        uint32_t b = (uint32_t)reinterpret_cast<const uint16_t*>(x)[idx] << 16;
+        f = __builtin_bit_cast(float, b);
+    } else {
+        f = reinterpret_cast<const float*>(x)[idx];
+    }
+    return (float)f32_to_f16_rne(f);
+}
+
+__device__ __forceinline__ void store_out(void* out, int dtype, int64_t idx, float v) {
+    if (dtype == kF32) {
+        reinterpret_cast<float*>(out)[idx] = v;
+    } else if (dtype == kF16) {
+        reinterpret_cast<uint16_t*>(out)[idx] = half_to_bits((half_t)v);
+    } else {
+        uint32_t b = __builtin_bit_cast(uint32_t, v);
+        b += 0x7FFFu + ((b >> 16) & 1u);  // RNE to bf16 (finite values)
+        reinterpret_cast<uint16_t*>(out)[idx] = (uint16_t)(b >> 16);
+    }
+}
+
+}  // namespace exl3

@@ -43,3 +43,91 @@ def activations(seed: int, rows: int, cols: int) -> np.ndarray:
     # round-to-nearest-even to bf16
     bits = ((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
     return bits.view(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Routed-expert layers and routing
+# ---------------------------------------------------------------------------
+
+def moe_layer(seed: int, n_experts: int, hidden: int, inter: int, K, gateless: bool = False) -> list:
+    """Per-expert packs: gate/up [hidden -> inter], down [inter -> hidden].
+
+    ``K`` is an int (uniform) or a per-expert sequence of ints or of
+    (K_gate, K_up, K_down) tuples."""
+    g = rng(seed)
+    experts = []
+    for e in range(n_experts):
+        ke = K if isinstance(K, int) else K[e]
+        kg, ku, kd = (ke, ke, ke) if isinstance(ke, (int, np.integer)) else tuple(ke)
+        pack = {}
+        if not gateless:
+            pack["gate"] = {"trellis": trellis(g, hidden, inter, int(kg)), "suh": suh(g, hidden),
+                            "svh": svh(g, inter), "K": int(kg)}
+        pack["up"] = {"trellis": trellis(g, hidden, inter, int(ku)), "suh": suh(g, hidden),
+                      "svh": svh(g, inter), "K": int(ku)}
+        pack["down"] = {"trellis": trellis(g, inter, hidden, int(kd)), "suh": suh(g, inter),
+                        "svh": svh(g, hidden), "K": int(kd)}
+        experts.append(pack)
+    return experts
+
+
+def mixed_k(seed: int, n_experts: int, probs=(0.4, 0.4, 0.2), ks=(2, 3, 4)) -> list:
+    """Per-expert K drawn from the seed (e.g. 40% K2 / 40% K3 / 20% K4)."""
+    return [int(k) for k in rng(seed).choice(ks, size=n_experts, p=probs)]
+
+
+def softmax_topk(seed: int, tokens: int, n_experts: int, topk: int):
+    """Router logits N(0,1) -> softmax -> top-k -> renormalised weights."""
+    logits = rng(seed).standard_normal((tokens, n_experts)).astype(np.float32)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :topk]
+    w = np.take_along_axis(p, ids, axis=1)
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    return ids.astype(np.int64), w
+
+
+def zipf_topk(seed: int, tokens: int, n_experts: int, topk: int, s: float = 1.1):
+    """Skewed routing: each token draws top-k distinct experts with
+    probability proportional to (rank+1)^-s over a seeded permutation of ids;
+    weights are a softmax of N(0,1) logits at the chosen ids."""
+    g = rng(seed)
+    perm = g.permutation(n_experts)
+    pr = (np.arange(n_experts) + 1.0) ** (-s)
+    pr /= pr.sum()
+    ids = np.empty((tokens, topk), dtype=np.int64)
+    for t in range(tokens):
+        ids[t] = perm[g.choice(n_experts, size=topk, replace=False, p=pr)]
+    logits = g.standard_normal((tokens, topk)).astype(np.float32)
+    w = np.exp(logits - logits.max(axis=1, keepdims=True))
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    return ids, w
+
+
+def to_device(experts: list, device) -> dict:
+    """Upload packs and build the nine int64 pointer tables plus int8 K tables.
+
+    The returned dict owns the device tensors (keep it alive while the tables
+    are in use)."""
+    import torch
+
+    store = []
+    names = ("gate", "up", "down")
+    gateless = "gate" not in experts[0]
+    tabs = {f"{p}_{a}": [] for p in names for a in ("trellis", "suh", "svh")}
+    ks = {p: [] for p in names}
+    for pack in experts:
+        for p in names:
+            src = pack["up"] if (p == "gate" and gateless) else pack[p]
+            t = torch.from_numpy(src["trellis"]).to(device)
+            su = torch.from_numpy(src["suh"]).to(device)
+            sv = torch.from_numpy(src["svh"]).to(device)
+            store += [t, su, sv]
+            tabs[f"{p}_trellis"].append(t.data_ptr())
+            tabs[f"{p}_suh"].append(su.data_ptr())
+            tabs[f"{p}_svh"].append(sv.data_ptr())
+            ks[p].append(src["K"])
+    out = {k: torch.tensor(v, dtype=torch.int64, device=device) for k, v in tabs.items()}
+    out["k_tables"] = tuple(torch.tensor(ks[p], dtype=torch.int8, device=device) for p in names)
+    out["_store"] = store
+    return out

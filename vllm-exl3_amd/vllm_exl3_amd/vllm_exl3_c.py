@@ -98,3 +98,299 @@ def decode_tiles(trellis: torch.Tensor, K: int, mcg: bool, *, mul1: bool = False
         _lib.call("exl3_decode_tiles", t.data_ptr(), t.size(0), t.size(1), K, cb,
                   out.data_ptr(), stream_of(dev))
     return out if trellis.is_cuda else out.to(trellis.device)
+
+
+# ---------------------------------------------------------------------------
+# Workspaces (no initialisation needed; split partials are finished by the
+# next kernel in stream order)
+# ---------------------------------------------------------------------------
+_WORKSPACES: dict[tuple, torch.Tensor] = {}
+
+_DTYPE_ID = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def _dtype_id(t: torch.Tensor, what: str) -> int:
+    if t.dtype not in _DTYPE_ID:
+        raise RuntimeError(f"{what} must be float16, bfloat16 or float32")
+    return _DTYPE_ID[t.dtype]
+
+
+def workspace(device: torch.device, kind: str, nbytes: int) -> torch.Tensor:
+    """Per-(device, kind) scratch, grown on demand.
+
+    Like the reference's process-global temp caches (src/vllm_exl3/exl3.py:
+    221-222, 2889) this is not thread-safe; calls sharing it must be ordered on
+    one stream.  Allocate outside graph capture (a first call sizes it)."""
+    key = (str(device), kind)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------------------
+# GEMV / GEMM
+# ---------------------------------------------------------------------------
+
+def _gemm_native(x2: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+                 K: int, cb: int, out_dtype: torch.dtype) -> torch.Tensor:
+    dev = x2.device
+    m, in_f = x2.shape
+    out_f = trellis.size(1) * 16
+    t = trellis.contiguous()
+    su = suh.reshape(-1).contiguous()
+    sv = svh.reshape(-1).contiguous()
+    out = torch.empty((m, out_f), dtype=out_dtype, device=dev)
+    lib = _lib.load()
+    need = int(lib.exl3_gemm_workspace_size(m, in_f, out_f))
+    ws = workspace(dev, "gemm", need)
+    with torch.cuda.device(dev):
+        _lib.call("exl3_gemm", x2.data_ptr(), _dtype_id(x2, "x"), m, t.data_ptr(), t.size(0),
+                  t.size(1), K, cb, su.data_ptr(), sv.data_ptr(), out.data_ptr(),
+                  _DTYPE_ID[out_dtype], ws.data_ptr(), ws.numel(), stream_of(dev))
+    return out
+
+
+def _check_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+                  K: int) -> None:
+    _check(K in (2, 3, 4), "native GEMV supports K in {2, 3, 4}")
+    _check(trellis.dim() == 3 and trellis.dtype == torch.int16 and trellis.size(2) == 16 * K,
+           "trellis must be int16 [rows/16, cols/16, 16*K]")
+    _check(x.size(-1) == trellis.size(0) * 16, "x feature dimension does not match trellis")
+    _check((trellis.size(0) * 16) % 128 == 0 and (trellis.size(1) * 16) % 128 == 0,
+           "trellis dimensions must reconstruct whole 128-element Hadamard blocks")
+    _check(suh.dtype == torch.float16 and svh.dtype == torch.float16, "suh and svh must be float16")
+    _check(suh.numel() == trellis.size(0) * 16 and svh.numel() == trellis.size(1) * 16,
+           "suh/svh do not match the trellis")
+
+
+def exl3_gemv(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+              K: int, mcg: bool, mmode: int = 1, *, mul1: bool = False,
+              codebook: int | None = None) -> torch.Tensor:
+    """Small-m GEMV with fused rotations.  csrc/bindings.cpp:134-147.
+
+    Returns fp16 [m, out] for device inputs; for host inputs the result comes
+    back in x's dtype on the host (the reference's CPU contract)."""
+    _check(x.dim() >= 2, "x must have shape [..., in_features]")
+    m = x.numel() // x.size(-1)
+    _check(1 <= m <= 8, "native GEMV supports 1 <= m <= 8")
+    _check(mmode in (0, 1), "mmode must be 0 or 1")
+    K = int(K)
+    _check_linear(x, trellis, suh, svh, K)
+    cb = codebook_id(mcg, mul1, codebook)
+    dev = _gpu_device(x)
+    x2 = x.to(dev).contiguous().view(m, x.size(-1))
+    out = _gemm_native(x2, trellis.to(dev), suh.to(dev), svh.to(dev), K, cb, torch.float16)
+    return out if x.is_cuda else out.to(x.device, x.dtype)
+
+
+def exl3_gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+              K: int, mcg: bool, *, mul1: bool = False, codebook: int | None = None,
+              out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Any-m EXL3 GEMM: fp16 [m, out].  csrc/bindings.cpp:110-115."""
+    K = int(K)
+    _check(x.dim() >= 1 and x.numel() > 0, "x must have shape [..., in_features]")
+    _check_linear(x, trellis, suh, svh, K)
+    cb = codebook_id(mcg, mul1, codebook)
+    dev = _gpu_device(x)
+    x2 = x.to(dev).contiguous().view(-1, x.size(-1))
+    out = _gemm_native(x2, trellis.to(dev), suh.to(dev), svh.to(dev), K, cb, out_dtype)
+    return out if x.is_cuda else out.to(x.device)
+
+
+# ---------------------------------------------------------------------------
+# Routed-expert MoE
+# ---------------------------------------------------------------------------
+ACT_SILU, ACT_RELU2, ACT_SWIGLU_OAI = 0, 2, 3
+
+
+def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+                tables: dict[str, torch.Tensor], n_local: int, intermediate_size: int, *,
+                K: tuple[int, int, int] = (4, 4, 4), k_tables: tuple | None = None,
+                codebook: int = CB_MCG, gateless: bool = False, act: int = ACT_SILU,
+                swiglu_limit: float = 0.0, n_valid: torch.Tensor | None = None,
+                out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """All T rows of a routed-expert layer in one launch sequence.
+
+    ``tables`` holds the nine int64 pointer tables (keys gate_trellis, gate_suh,
+    gate_svh, up_*, down_*), one entry per local expert.  ``ids`` [T, topk]
+    local ids; ids outside [0, n_local) are skipped.  Returns [T, hidden]."""
+    _check(x.dim() == 2 and x.is_cuda, "fused MoE requires a CUDA [T, hidden] input")
+    T, hidden = x.shape
+    _check(ids.dim() == 2 and ids.size(0) == T, "fused MoE ids must be [T, topk]")
+    _check(ids.dtype in (torch.int32, torch.int64), "fused MoE ids must be int32 or int64")
+    topk = ids.size(1)
+    _check(weights.shape == ids.shape, "fused MoE requires one routing weight per expert index")
+    dev = x.device
+    xs = x.contiguous()
+    ids_c = ids.contiguous()
+    w_c = weights.contiguous()
+    names = ("gate_trellis", "gate_suh", "gate_svh", "up_trellis", "up_suh", "up_svh",
+             "down_trellis", "down_suh", "down_svh")
+    ptrs = []
+    for nm in names:
+        t = tables.get(nm)
+        if t is None:
+            _check(gateless and nm.startswith("gate"), f"fused MoE pointer table {nm} missing")
+            ptrs.append(None)
+            continue
+        _check(t.dim() == 1 and t.dtype == torch.int64 and t.is_contiguous() and t.device == dev,
+               "fused MoE pointer tables must be contiguous int64 vectors on the input device")
+        _check(t.numel() >= n_local, "fused MoE n_local must bound the pointer tables")
+        ptrs.append(t.data_ptr())
+    kt = [None, None, None]
+    if k_tables is not None:
+        for i, t in enumerate(k_tables):
+            if t is None:
+                continue
+            _check(t.dtype == torch.int8 and t.dim() == 1 and t.is_contiguous() and t.device == dev
+                   and t.numel() >= n_local,
+                   "fused MoE requires int8 device K tables with one entry per pointer-table slot")
+            kt[i] = t.data_ptr()
+    if n_valid is not None:
+        _check(n_valid.is_cuda and n_valid.dtype == torch.int32 and n_valid.numel() == 1
+               and n_valid.is_contiguous() and n_valid.device == dev,
+               "padded fused MoE requires a contiguous int32 CUDA n_valid scalar tensor on x.device()")
+    if out is None:
+        out = torch.empty((T, hidden), dtype=out_dtype, device=dev)
+    _check(out.shape == (T, hidden) and out.is_contiguous() and out.device == dev,
+           "fused MoE output shape must match input")
+    lib = _lib.load()
+    need = int(lib.exl3_moe_workspace_size(T, topk, n_local, hidden, intermediate_size, int(gateless)))
+    _check(need > 0, "fused MoE: unsupported geometry")
+    ws = workspace(dev, "moe", need)
+    with torch.cuda.device(dev):
+        _lib.call("exl3_moe_forward", xs.data_ptr(), _dtype_id(xs, "x"), T, hidden,
+                  int(intermediate_size), *ptrs, int(n_local), kt[0], kt[1], kt[2],
+                  int(K[0]), int(K[1]), int(K[2]), int(codebook), int(gateless), int(act),
+                  float(swiglu_limit), ids_c.data_ptr(), 1 if ids_c.dtype == torch.int64 else 0,
+                  w_c.data_ptr(), _dtype_id(w_c, "routing weights"), topk,
+                  n_valid.data_ptr() if n_valid is not None else None, out.data_ptr(),
+                  _dtype_id(out, "out"), ws.data_ptr(), ws.numel(), stream_of(dev))
+    return out
+
+
+def _check_fused_common(prefix: str, x, out, ptr_tables, intermediate_size, swiglu_limit) -> None:
+    _check(x.is_cuda and x.dtype == torch.float16, f"{prefix} requires CUDA fp16 input")
+    _check(out.is_cuda and out.dtype == torch.float16, f"{prefix} output must be CUDA fp16")
+    _check(out.shape == x.shape, f"{prefix} output shape must match input")
+    _check(x.dim() == 2 and x.size(1) > 0 and x.size(1) % 128 == 0,
+           f"{prefix} hidden width must be a positive multiple of 128")
+    _check(intermediate_size > 0 and intermediate_size % 128 == 0,
+           f"{prefix} local intermediate width must be a positive multiple of 128")
+    _check(math.isfinite(swiglu_limit) and swiglu_limit >= 0.0,
+           f"{prefix} SwiGLU limit must be finite and nonnegative (0 disables clipping)")
+    n = ptr_tables[0].numel()
+    for t in ptr_tables:
+        _check(t.dim() == 1 and t.dtype == torch.int64 and t.numel() == n and n > 0,
+               f"{prefix} pointer tables must be equally sized nonempty int64 vectors")
+    for t in (x, out, *ptr_tables):
+        _check(t.device == x.device and t.is_contiguous(),
+               f"{prefix} tensors must be contiguous and on the input CUDA device")
+
+
+def _tables_dict(gt, gu, gv, ut, uu, uv, dt, du, dv) -> dict:
+    return {"gate_trellis": gt, "gate_suh": gu, "gate_svh": gv, "up_trellis": ut, "up_suh": uu,
+            "up_svh": uv, "down_trellis": dt, "down_suh": du, "down_svh": dv}
+
+
+def p2b_fused_moe(x: torch.Tensor, out: torch.Tensor, gate_trellis_ptrs, gate_suh_ptrs,
+                  gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs, down_trellis_ptrs,
+                  down_suh_ptrs, down_svh_ptrs, expert_indices: torch.Tensor,
+                  routing_weights: torch.Tensor, K_gate: int, K_up: int, K_down: int, mcg: bool,
+                  intermediate_size: int = 2048, swiglu_limit: float = 0.0, *,
+                  codebook: int | None = None) -> torch.Tensor:
+    """One-row fused decode MoE, written into ``out`` in place.
+
+    csrc/bindings.cpp:158-167 / csrc/p2b_moe.cu:2431-2487 (uniform K; ids index
+    the pointer tables directly; combine in slot order)."""
+    tabs = (gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs,
+            up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs)
+    _check_fused_common("fused MoE", x, out, tabs, intermediate_size, swiglu_limit)
+    _check(x.size(0) == 1, "fused MoE requires exactly one input row")
+    _check(K_gate == K_up == K_down and K_gate in (2, 3, 4),
+           "unsupported fused MoE K (uniform K in {2, 3, 4} required)")
+    _check(expert_indices.dim() == 1 and expert_indices.dtype == torch.int32
+           and expert_indices.numel() > 0,
+           "fused MoE expert indices must be a nonempty int32 routing vector")
+    _check(routing_weights.dtype == torch.float16
+           and routing_weights.numel() == expert_indices.numel(),
+           "fused MoE requires one fp16 routing weight per expert index")
+    _check(expert_indices.device == x.device and routing_weights.device == x.device
+           and expert_indices.is_contiguous() and routing_weights.is_contiguous(),
+           "fused MoE tensors must be contiguous and on the input CUDA device")
+    cb = codebook_id(mcg, False, codebook)
+    moe_forward(x, expert_indices.view(1, -1), routing_weights.view(1, -1), _tables_dict(*tabs),
+                gate_trellis_ptrs.numel(), intermediate_size, K=(K_gate, K_up, K_down),
+                codebook=cb, swiglu_limit=swiglu_limit, out=out)
+    return out
+
+
+def p2b_fused_moe_mk(x: torch.Tensor, out: torch.Tensor, gate_trellis_ptrs, gate_suh_ptrs,
+                     gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs, down_trellis_ptrs,
+                     down_suh_ptrs, down_svh_ptrs, expert_indices: torch.Tensor,
+                     routing_weights: torch.Tensor, k_gate_tbl: torch.Tensor,
+                     k_up_tbl: torch.Tensor, k_down_tbl: torch.Tensor, n_local: int, mcg: bool,
+                     intermediate_size: int = 2048, swiglu_limit: float = 0.0, *,
+                     codebook: int | None = None) -> torch.Tensor:
+    """One-row mixed-K fused decode MoE with int8 per-expert K tables and the
+    ``n_local`` sentinel.  csrc/bindings.cpp:169-180 / csrc/p2b_moe.cu:1201-1265."""
+    tabs = (gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs,
+            up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs)
+    pre = "mixed-K fused MoE"
+    _check_fused_common(pre, x, out, tabs, intermediate_size, swiglu_limit)
+    _check(x.size(0) == 1, f"{pre} requires exactly one input row")
+    _check(expert_indices.dim() == 1 and expert_indices.dtype == torch.int32
+           and expert_indices.numel() > 0,
+           f"{pre} expert indices must be a nonempty int32 routing vector")
+    _check(routing_weights.dtype == torch.float16
+           and routing_weights.numel() == expert_indices.numel(),
+           f"{pre} requires one fp16 routing weight per expert index")
+    for t in (k_gate_tbl, k_up_tbl, k_down_tbl):
+        _check(t.is_cuda and t.dim() == 1 and t.is_contiguous() and t.dtype == torch.int8
+               and t.numel() == gate_trellis_ptrs.numel(),
+               f"{pre} requires int8 CUDA K tables with one entry per pointer-table slot")
+    _check(1 <= n_local <= gate_trellis_ptrs.numel(),
+           f"{pre} n_local must bound the pointer tables (1 <= n_local <= table length)")
+    cb = codebook_id(mcg, False, codebook)
+    moe_forward(x, expert_indices.view(1, -1), routing_weights.view(1, -1), _tables_dict(*tabs),
+                int(n_local), intermediate_size, k_tables=(k_gate_tbl, k_up_tbl, k_down_tbl),
+                codebook=cb, swiglu_limit=swiglu_limit, out=out)
+    return out
+
+
+def p2b_fused_moe_padded(x: torch.Tensor, out: torch.Tensor, gate_trellis_ptrs, gate_suh_ptrs,
+                         gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs,
+                         down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs,
+                         expert_indices_padded: torch.Tensor, routing_weights_padded: torch.Tensor,
+                         n_valid: torch.Tensor, k_gate_tbl: torch.Tensor, k_up_tbl: torch.Tensor,
+                         k_down_tbl: torch.Tensor, n_local: int, max_k: int, mcg: bool,
+                         intermediate_size: int = 2048, swiglu_limit: float = 0.0, *,
+                         codebook: int | None = None) -> torch.Tensor:
+    """Fixed-shape [MAX_T, MAX_K] decode MoE whose live row count is the device
+    scalar ``n_valid`` (never read on the host); padded rows come out as exact
+    zeros.  csrc/bindings.cpp:182-195 / csrc/p2b_moe.cu:2346-2428."""
+    tabs = (gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs,
+            up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs)
+    pre = "padded fused MoE"
+    _check_fused_common(pre, x, out, tabs, intermediate_size, swiglu_limit)
+    _check(expert_indices_padded.dim() == 2 and expert_indices_padded.dtype == torch.int32
+           and expert_indices_padded.size(0) == x.size(0) and expert_indices_padded.size(1) >= 1,
+           f"{pre} requires an int32 [MAX_T, MAX_K] routing grid whose rows match x")
+    _check(routing_weights_padded.dtype == torch.float16
+           and routing_weights_padded.shape == expert_indices_padded.shape,
+           f"{pre} requires one fp16 routing weight per routing-grid slot")
+    for t in (k_gate_tbl, k_up_tbl, k_down_tbl):
+        _check(t.is_cuda and t.dim() == 1 and t.is_contiguous() and t.dtype == torch.int8
+               and t.numel() == gate_trellis_ptrs.numel(),
+               f"{pre} requires int8 CUDA K tables with one entry per pointer-table slot")
+    _check(1 <= n_local <= gate_trellis_ptrs.numel(),
+           f"{pre} n_local must bound the pointer tables (1 <= n_local <= table length)")
+    _check(max_k == expert_indices_padded.size(1),
+           f"{pre} max_k must equal the routing grid's column count")
+    cb = codebook_id(mcg, False, codebook)
+    moe_forward(x, expert_indices_padded, routing_weights_padded, _tables_dict(*tabs),
+                int(n_local), intermediate_size, k_tables=(k_gate_tbl, k_up_tbl, k_down_tbl),
+                codebook=cb, swiglu_limit=swiglu_limit, n_valid=n_valid, out=out)
+    return out
