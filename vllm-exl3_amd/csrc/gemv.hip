@@ -23,6 +23,7 @@ namespace exl3 {
 namespace {
 
 constexpr int kMaxMRB = 16;       // activation rows per row group (one MFMA row block)
+constexpr int kMoeMRB = 8;        // row-group size of the MoE phases
 constexpr int kMaxRoutes = 8192;  // routes sortable by the single-workgroup router
 constexpr int kRouteBits = 13;    // log2(kMaxRoutes)
 constexpr int kRouteThreads = 1024;
@@ -39,56 +40,89 @@ __device__ __forceinline__ half8_t dup4(uint32_t d0, uint32_t d1) {
     return __builtin_bit_cast(half8_t, r);
 }
 
+typedef __attribute__((address_space(1))) const v4u* gv4p;
+
 // Stream the wave's tile rows of one projection for the current chunk and
 // accumulate into acc[8] (one float4 per 16-column tile).
 //   tbase:     byte address of tile (first tile row of the chunk, j*8)
 //   row_bytes: bytes between consecutive tile rows (tiles_n * 32K)
 //   nkt:       tile rows in the chunk; the wave takes rows wave, wave+4, ...
 //   A:         this projection's activations [nkt][MRB][16] fp16 (kappa order)
-template <int K, int CB>
-__device__ __forceinline__ void stream_rows(const uint8_t* __restrict__ tbase, size_t row_bytes,
-                                            int nkt, int wave, int lane, uint32_t* stage,
-                                            const uint16_t* A, int MRB, int arow,
-                                            float4_t (&acc)[8]) {
-    constexpr int span = 256 * K;
-    constexpr int tile_bytes = 32 * K;
-    const bool ld = lane * 16 < span;
-    const LaneWords lw = lane_words<K>(lane);
-    const int g = lane >> 4;
-    const int n = nkt > wave ? (nkt - wave + kWaves - 1) / kWaves : 0;
-    const uint8_t* lane_base = tbase + lane * 16;
+// The pipeline keeps kDepth rows in flight.  Its steady state has no
+// branches: lanes past the 256*K-byte row span reload the span's first 16
+// bytes, prefetches past the last row reload the last row (all in bounds),
+// and every lane stores into the 1 KB stage (bytes past the span are never
+// read).
+template <int K>
+struct RowStream {
+    const uint8_t* lane_base;  // this lane's 16 bytes of the wave's first row
+    size_t step;               // bytes between the wave's consecutive rows
+    int n;                     // rows of this wave in the chunk
     v4u buf[kDepth];
+};
+
+// Issue the loads of the wave's first kDepth rows (clamped, in bounds) so
+// they are in flight while the activations are staged.
+template <int K>
+__device__ __forceinline__ void stream_prefetch(RowStream<K>& rs, const uint8_t* tbase,
+                                                size_t row_bytes, int nkt, int wave, int lane) {
+    constexpr int span = 256 * K;
+    rs.n = nkt > wave ? (nkt - wave + kWaves - 1) / kWaves : 0;
+    rs.lane_base = tbase + (lane * 16 < span ? lane * 16 : 0) + (size_t)wave * row_bytes;
+    rs.step = row_bytes * kWaves;
+    if (rs.n == 0) return;
 #pragma unroll
     for (int d = 0; d < kDepth; ++d)
-        if (d < n && ld)
-            buf[d] = __builtin_nontemporal_load(
-                reinterpret_cast<const v4u*>(lane_base + (size_t)(wave + d * kWaves) * row_bytes));
+        rs.buf[d] = __builtin_nontemporal_load((gv4p)(rs.lane_base + (size_t)min(d, rs.n - 1) * rs.step));
+}
+
+// Consume the wave's rows: per row, stage 256*K bytes in LDS, refill the
+// pipeline, read the sixteen words this lane needs, decode and issue eight
+// MFMAs.  The steady state has no branches: lanes past the row span reload
+// its first 16 bytes, prefetches past the last row reload the last row (all
+// in bounds), and every lane stores into the 1 KB stage (bytes past the span
+// are never read).
+template <int K, int CB>
+__device__ __forceinline__ void stream_consume(RowStream<K>& rs, int wave, int lane, uint32_t* stage,
+                                               const uint16_t* A, int MRB, int arow,
+                                               float4_t (&acc)[8]) {
+    constexpr int tile_bytes = 32 * K;
+    const int n = rs.n;
+    if (n == 0) return;
+    const LaneWords lw = lane_words<K>(lane);
+    const int g = lane >> 4;
     const uint8_t* st = reinterpret_cast<const uint8_t*>(stage);
-    for (int i0 = 0; i0 < n; i0 += kDepth) {
+    const uint32_t* arow_p = reinterpret_cast<const uint32_t*>(A + (size_t)arow * 16 + 4 * g) +
+                             (size_t)wave * MRB * 8;
+    const int a_step = kWaves * MRB * 8;  // uint32 words between this wave's consecutive rows
+    auto consume = [&](int d, int i) {
+        reinterpret_cast<v4u*>(stage)[lane] = rs.buf[d];
+        rs.buf[d] = __builtin_nontemporal_load(
+            (gv4p)(rs.lane_base + (size_t)min(i + kDepth, n - 1) * rs.step));
+        const uint32_t* ap = arow_p + (size_t)i * a_step;
+        // all sixteen words of the row first: one LDS latency per row
+        uint32_t wh[8], wl[8];
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d) {
-            const int i = i0 + d;
-            if (i < n) {
-                if (ld) reinterpret_cast<v4u*>(stage)[lane] = buf[d];
-                const int inext = i + kDepth;
-                if (inext < n && ld)
-                    buf[d] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(
-                        lane_base + (size_t)(wave + inext * kWaves) * row_bytes));
-                const int ktl = wave + i * kWaves;
-                const uint32_t* ap =
-                    reinterpret_cast<const uint32_t*>(A + ((size_t)ktl * MRB + arow) * 16 + 4 * g);
-                const half8_t a = dup4(ap[0], ap[1]);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const uint32_t hi = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_hi);
-                    const uint32_t lo = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_lo);
-                    uint32_t b[4];
-                    decode4<K, CB>(hi, lo, lw.shift, b);
-                    acc[t] = mfma16x16x32(a, b, acc[t]);
-                }
-            }
+        for (int t = 0; t < 8; ++t) {
+            wh[t] = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_hi);
+            wl[t] = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_lo);
         }
+        const half8_t a = dup4(ap[0], ap[1]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t b[4];
+            decode4<K, CB>(wh[t], wl[t], lw.shift, b);
+            acc[t] = mfma16x16x32(a, b, acc[t]);
+        }
+    };
+    int i = 0;
+    for (; i + kDepth <= n; i += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) consume(d, i + d);
     }
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d)
+        if (i + d < n) consume(d, i + d);
 }
 
 struct Proj {
@@ -116,6 +150,30 @@ __device__ __forceinline__ float activate(float g, float u, int act, float limit
     return silu_f(g) * u;
 }
 
+// Sum of the S split partials at columns c0 and c0 + 64 of one row, in split
+// order (deterministic), with the loads of up to 8 splits issued together.
+__device__ __forceinline__ void sum_splits(const float* __restrict__ base, int64_t split_stride,
+                                           int S, int c0, float& v0, float& v1) {
+    int ss = 0;
+    for (; ss + 8 <= S; ss += 8) {
+        float a[8], b[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            a[i] = base[(ss + i) * split_stride + c0];
+            b[i] = base[(ss + i) * split_stride + c0 + 64];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v0 += a[i];
+            v1 += b[i];
+        }
+    }
+    for (; ss < S; ++ss) {
+        v0 += base[ss * split_stride + c0];
+        v1 += base[ss * split_stride + c0 + 64];
+    }
+}
+
 // Output side of one 128-column block for one row: v[h] holds the summed,
 // not yet rotated result at column lane + 64 h; returns (H v / sqrt(128)) * svh.
 __device__ __forceinline__ void finish_block(float& v0, float& v1, const uint16_t* svh, int c0,
@@ -138,14 +196,13 @@ __device__ __forceinline__ void gateup_finish(const GemvParams& p, const Proj* g
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         if (q < nproj) {
-            for (int ss = 0; ss < p.src_S; ++ss) {
-                const float* src = p.src_ws + (((int64_t)q * p.src_S + ss) * p.n_rows_ws + row) * inter;
-                v[q][0] += src[c0];
-                v[q][1] += src[c0 + 64];
-            }
-            finish_block(v[q][0], v[q][1], gu[q].svh, c0, lane);
+            sum_splits(p.src_ws + ((int64_t)q * p.src_S * p.n_rows_ws + row) * inter,
+                       (int64_t)p.n_rows_ws * inter, p.src_S, c0, v[q][0], v[q][1]);
         }
     }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+        if (q < nproj) finish_block(v[q][0], v[q][1], gu[q].svh, c0, lane);
     float a[2];
     for (int h = 0; h < 2; ++h) {
         const float u = (float)f32_to_f16_rne(nproj == 2 ? v[1][h] : v[0][h]);
@@ -159,29 +216,138 @@ __device__ __forceinline__ void gateup_finish(const GemvParams& p, const Proj* g
     a1 = a[1] * kHadNorm;
 }
 
+// Everything one projection of one row group needs, shared by all waves.
+struct RowGroup {
+    int rg, nr, arow, row_base, hb_first, j, tiles_n, expert;
+};
+
+// Stage the rotated activations of one projection for chunk [c0, c0 + nb)
+// of 128-row blocks, stream its tiles, and add the result into red[row][128]
+// (waves in fixed order).  acc lives only inside this K-specialised routine.
+template <int K, int CB, int MODE>
+__device__ __forceinline__ void run_projection(const GemvParams& p, const RowGroup& G, const Proj& pq,
+                                               const Proj* gu, const uint16_t* down_suh,
+                                               uint32_t* stage, uint16_t* A, float* red, int wave,
+                                               int lane) {
+    float4_t acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int MRB = p.MRB;
+    const int gu_nproj = p.gateless ? 1 : 2;
+    constexpr size_t tile_bytes = 32u * K;
+    const size_t row_bytes = (size_t)G.tiles_n * tile_bytes;
+    for (int c0 = 0; c0 < p.R_hb; c0 += p.C_hb) {
+        const int nb = min(p.C_hb, p.R_hb - c0);
+        // trellis bytes of this chunk start moving before the staging below
+        RowStream<K> rs;
+        const uint8_t* tb = pq.trellis +
+                            ((size_t)(G.hb_first + c0) * 8 * G.tiles_n + (size_t)G.j * 8) * tile_bytes;
+        stream_prefetch<K>(rs, tb, row_bytes, nb * 8, wave, lane);
+        __syncthreads();
+        const int units = G.nr * nb;
+        if constexpr (MODE == kModeDown) {
+            for (int u = wave; u < units; u += kWaves) {
+                const int r = u / nb, hb = u % nb;
+                float v0, v1;
+                gateup_finish(p, gu, gu_nproj, down_suh, G.row_base + G.rg + r, G.hb_first + c0 + hb,
+                              lane, v0, v1);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int c = lane + 64 * h;
+                    A[((hb * 8 + (c >> 4)) * MRB + r) * 16 + pi_inv(c & 15)] =
+                        half_to_bits(f32_to_f16_rne(h ? v1 : v0));
+                }
+            }
+        } else {
+            // up to kUnitBatch units per wave: issue every load, then rotate
+            constexpr int kUnitBatch = 4;
+            for (int u0 = wave; u0 < units; u0 += kWaves * kUnitBatch) {
+                float xv[kUnitBatch][2], sv[kUnitBatch][2];
+#pragma unroll
+                for (int b = 0; b < kUnitBatch; ++b) {
+                    const int u = u0 + b * kWaves;
+                    if (u < units) {
+                        const int r = u / nb, hb = u % nb;
+                        const int64_t fb = (int64_t)(G.hb_first + c0 + hb) * 128;
+                        int64_t tok;
+                        if constexpr (MODE == kModeLinear)
+                            tok = G.rg + r;
+                        else
+                            tok = p.row_token[G.row_base + G.rg + r];
+                        xv[b][0] = load_act(p.x, p.x_dtype, tok * p.x_stride + fb + lane);
+                        xv[b][1] = load_act(p.x, p.x_dtype, tok * p.x_stride + fb + lane + 64);
+                        sv[b][0] = (float)bits_to_half(pq.suh[fb + lane]);
+                        sv[b][1] = (float)bits_to_half(pq.suh[fb + lane + 64]);
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < kUnitBatch; ++b) {
+                    const int u = u0 + b * kWaves;
+                    if (u < units) {
+                        const int r = u / nb, hb = u % nb;
+                        float v0 = xv[b][0] * sv[b][0], v1 = xv[b][1] * sv[b][1];
+                        had128(v0, v1, lane);
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int c = lane + 64 * h;
+                            A[((hb * 8 + (c >> 4)) * MRB + r) * 16 + pi_inv(c & 15)] =
+                                half_to_bits(f32_to_f16_rne((h ? v1 : v0) * kHadNorm));
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        stream_consume<K, CB>(rs, wave, lane, stage, A, MRB, G.arow, acc);
+    }
+    // cross-wave reduction, fixed wave order (every wave has finished reading
+    // A once it reaches the first barrier below)
+    const int g = lane >> 4;
+    const int col_nu = sigma_col(lane & 15);
+    for (int w = 0; w < kWaves; ++w) {
+        if (wave == w) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 4 * g + i;
+                    if (row < G.nr) {
+                        float* dst = red + row * 128 + t * 16 + col_nu;
+                        *dst = (w == 0 ? 0.0f : *dst) + acc[t][i];
+                    }
+                }
+        }
+        __syncthreads();
+    }
+}
+
 template <int CB, int MODE>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemv_kernel(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nJ = p.out_features >> 7;
+    // gate/up: each workgroup streams one of the two projections
+    const int nsplit_proj = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
     const int item = blockIdx.x;
-    const int s = item % p.S;
-    const int rest = item / p.S;
-    const int j = rest % nJ;
+    const int qsel = item % nsplit_proj;
+    const int s = (item / nsplit_proj) % p.S;
+    const int rest = item / nsplit_proj / p.S;
+    RowGroup G;
+    G.j = rest % nJ;
     const int slot = rest / nJ;
 
-    int rows, row_base, expert = 0;
+    int rows;
+    G.expert = 0;
     if constexpr (MODE == kModeLinear) {
         rows = p.m_rows;
-        row_base = 0;
+        G.row_base = 0;
     } else {
         if (slot >= *p.n_active) return;
-        expert = p.slot_expert[slot];
-        row_base = p.slot_start[slot];
+        G.expert = p.slot_expert[slot];
+        G.row_base = p.slot_start[slot];
         rows = p.slot_rows[slot];
     }
-    // projections streamed by this kernel
-    const int nproj = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
+    const int nproj = 1;  // projections streamed by this workgroup
     Proj pr[2];
     // Down: gate/up projections whose partials are finished while staging
     Proj gu[2];
@@ -192,15 +358,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
     } else {
         auto load_proj = [&](int pj) {
             Proj q;
-            q.trellis = reinterpret_cast<const uint8_t*>(p.tab[3 * pj][expert]);
-            q.suh = reinterpret_cast<const uint16_t*>(p.tab[3 * pj + 1][expert]);
-            q.svh = reinterpret_cast<const uint16_t*>(p.tab[3 * pj + 2][expert]);
-            q.K = p.ktab[pj] ? (int)p.ktab[pj][expert] : p.kuni[pj];
+            q.trellis = reinterpret_cast<const uint8_t*>(p.tab[3 * pj][G.expert]);
+            q.suh = reinterpret_cast<const uint16_t*>(p.tab[3 * pj + 1][G.expert]);
+            q.svh = reinterpret_cast<const uint16_t*>(p.tab[3 * pj + 2][G.expert]);
+            q.K = p.ktab[pj] ? (int)p.ktab[pj][G.expert] : p.kuni[pj];
             return q;
         };
         if constexpr (MODE == kModeGateUp) {
-            pr[0] = load_proj(p.gateless ? 1 : 0);
-            pr[1] = load_proj(1);
+            pr[0] = load_proj(p.gateless ? 1 : qsel);
+            pr[1] = pr[0];
         } else {
             pr[0] = load_proj(2);
             pr[1] = pr[0];
@@ -209,119 +375,42 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
             down_suh = pr[0].suh;
         }
     }
-    const int gu_nproj = p.gateless ? 1 : 2;
 
     const int MRB = p.MRB;
-    const int tiles_n = p.out_features >> 4;
-    const int hb_first = s * p.R_hb;  // first 128-row input block of this split
+    G.tiles_n = p.out_features >> 4;
+    G.hb_first = s * p.R_hb;  // first 128-row input block of this split
+    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16][red: nproj x MRB x 128 fp32]
     uint32_t* stage = reinterpret_cast<uint32_t*>(lds) + wave * (kStageBytes / 4);
     uint16_t* A = reinterpret_cast<uint16_t*>(lds + kWaves * kStageBytes);
-    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes);
-    const int g = lane >> 4, nu = lane & 15;
-    const int col_nu = sigma_col(nu);
+    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes + (size_t)p.C_hb * 8 * MRB * 32);
 
-    for (int rg = 0; rg < rows; rg += MRB) {
-        const int nr = min(MRB, rows - rg);
-        const int arow = min(lane & 15, nr - 1);
-        float4_t acc[2][8];
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-#pragma unroll
-            for (int t = 0; t < 8; ++t) acc[q][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-        for (int c0 = 0; c0 < p.R_hb; c0 += p.C_hb) {
-            const int nb = min(p.C_hb, p.R_hb - c0);
-            const int qstride = nb * 8 * MRB * 16;  // fp16 elements per projection block
-            __syncthreads();
-            // ---- activations of this chunk, rotated, into LDS ----
-            const int units = nproj * nr * nb;
-            for (int u = wave; u < units; u += kWaves) {
-                const int q = u / (nr * nb);
-                const int r = (u / nb) % nr;
-                const int hb = u % nb;
-                const int64_t fb = (int64_t)(hb_first + c0 + hb) * 128;
-                float v0, v1;
-                if constexpr (MODE == kModeDown) {
-                    gateup_finish(p, gu, gu_nproj, down_suh, row_base + rg + r, hb_first + c0 + hb,
-                                  lane, v0, v1);
-                } else {
-                    int64_t tok;
-                    if constexpr (MODE == kModeLinear)
-                        tok = rg + r;
-                    else
-                        tok = p.row_token[row_base + rg + r];
-                    v0 = load_act(p.x, p.x_dtype, tok * p.x_stride + fb + lane);
-                    v1 = load_act(p.x, p.x_dtype, tok * p.x_stride + fb + lane + 64);
-                    const uint16_t* su = q ? pr[1].suh : pr[0].suh;
-                    v0 *= (float)bits_to_half(su[fb + lane]);
-                    v1 *= (float)bits_to_half(su[fb + lane + 64]);
-                    had128(v0, v1, lane);
-                    v0 *= kHadNorm;
-                    v1 *= kHadNorm;
-                }
-                uint16_t* Aq = A + q * qstride;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int c = lane + 64 * h;
-                    const int ktl = hb * 8 + (c >> 4);
-                    Aq[(ktl * MRB + r) * 16 + pi_inv(c & 15)] =
-                        half_to_bits(f32_to_f16_rne(h ? v1 : v0));
-                }
+    for (G.rg = 0; G.rg < rows; G.rg += MRB) {
+        G.nr = min(MRB, rows - G.rg);
+        G.arow = min(lane & 15, G.nr - 1);
+        for (int q = 0; q < nproj; ++q) {
+            const Proj pq = q ? pr[1] : pr[0];
+            float* rq = red + q * MRB * 128;
+            switch (pq.K) {
+                case 2: run_projection<2, CB, MODE>(p, G, pq, gu, down_suh, stage, A, rq, wave, lane); break;
+                case 3: run_projection<3, CB, MODE>(p, G, pq, gu, down_suh, stage, A, rq, wave, lane); break;
+                case 4: run_projection<4, CB, MODE>(p, G, pq, gu, down_suh, stage, A, rq, wave, lane); break;
+                default: break;  // rejected on the host
             }
-            __syncthreads();
-            // ---- stream the packed tiles of each projection ----
-            // (projection index kept compile-time so acc stays in registers)
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                if (q < nproj) {
-                    const size_t tile_bytes = 32u * (size_t)pr[q].K;
-                    const size_t row_bytes = (size_t)tiles_n * tile_bytes;
-                    const uint8_t* tb = pr[q].trellis + ((size_t)(hb_first + c0) * 8 * tiles_n +
-                                                         (size_t)j * 8) * tile_bytes;
-                    const uint16_t* Aq = A + q * qstride;
-                    switch (pr[q].K) {
-                        case 2: stream_rows<2, CB>(tb, row_bytes, nb * 8, wave, lane, stage, Aq, MRB, arow, acc[q]); break;
-                        case 3: stream_rows<3, CB>(tb, row_bytes, nb * 8, wave, lane, stage, Aq, MRB, arow, acc[q]); break;
-                        case 4: stream_rows<4, CB>(tb, row_bytes, nb * 8, wave, lane, stage, Aq, MRB, arow, acc[q]); break;
-                        default: break;  // rejected on the host
-                    }
-                }
-            }
-        }
-        // ---- cross-wave reduction into red[q][row][128], fixed wave order ----
-        __syncthreads();
-        for (int w = 0; w < kWaves; ++w) {
-            if (wave == w) {
-#pragma unroll
-                for (int q = 0; q < 2; ++q)
-                    if (q < nproj)
-#pragma unroll
-                        for (int t = 0; t < 8; ++t)
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const int row = 4 * g + i;
-                                if (row < nr) {
-                                    float* dst = red + (q * MRB + row) * 128 + t * 16 + col_nu;
-                                    *dst = (w == 0 ? 0.0f : *dst) + acc[q][t][i];
-                                }
-                            }
-            }
-            __syncthreads();
         }
         if (MODE == kModeLinear && p.S == 1) {
             // single split: finish in place
-            for (int r = wave; r < nr; r += kWaves) {
+            for (int r = wave; r < G.nr; r += kWaves) {
                 float v0 = red[r * 128 + lane], v1 = red[r * 128 + lane + 64];
-                finish_block(v0, v1, pr[0].svh, j * 128 + lane, lane);
-                const int64_t o = (int64_t)(rg + r) * p.out_stride + j * 128 + lane;
+                finish_block(v0, v1, pr[0].svh, G.j * 128 + lane, lane);
+                const int64_t o = (int64_t)(G.rg + r) * p.out_stride + G.j * 128 + lane;
                 store_out(p.out, p.out_dtype, o, v0);
                 store_out(p.out, p.out_dtype, o + 64, v1);
             }
         } else {
-            for (int e = tid; e < nproj * nr * 128; e += kThreads) {
-                const int q = e / (nr * 128), r = (e >> 7) % nr, c = e & 127;
-                p.ws[(((int64_t)q * p.S + s) * p.n_rows_ws + row_base + rg + r) * p.out_features +
-                     j * 128 + c] = red[(q * MRB + r) * 128 + c];
+            for (int e = tid; e < G.nr * 128; e += kThreads) {
+                const int r = e >> 7, c = e & 127;
+                p.ws[(((int64_t)qsel * p.S + s) * p.n_rows_ws + G.row_base + G.rg + r) * p.out_features +
+                     G.j * 128 + c] = red[r * 128 + c];
             }
         }
         __syncthreads();
@@ -340,11 +429,7 @@ __global__ __launch_bounds__(256) void linear_finish_kernel(const float* __restr
     if (item >= m * nJ) return;
     const int r = item / nJ, j = item % nJ;
     float v0 = 0.f, v1 = 0.f;
-    for (int ss = 0; ss < S; ++ss) {
-        const float* src = ws + ((int64_t)ss * m + r) * out_f + j * 128;
-        v0 += src[lane];
-        v1 += src[lane + 64];
-    }
+    sum_splits(ws + (int64_t)r * out_f, (int64_t)m * out_f, S, j * 128 + lane, v0, v1);
     finish_block(v0, v1, svh, j * 128 + lane, lane);
     const int64_t o = (int64_t)r * out_f + j * 128 + lane;
     store_out(out, out_dtype, o, v0);
@@ -457,51 +542,56 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const void* ids, i
 
 // out[t, block j] = sum_k w[t,k] * finish(sum_s partial_s[pos(t,k)]) in slot
 // order; sentinel routes are skipped (their rows are never read, so unwritten
-// rows cannot leak NaN).  One wave per (token, 128-column block).
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ ws, int S,
-                                                     int n_routes, int H, const int* route_pos,
-                                                     const int* row_expert,
-                                                     const int64_t* down_svh_tab,
-                                                     const void* weights, int w_dtype, int T,
-                                                     int topk, void* out, int out_dtype) {
-    const int lane = threadIdx.x & 63;
+// rows cannot leak NaN).  One workgroup per (token, 128-column block); wave k
+// finishes routes k, k + waves, ...; the weighted results meet in LDS and are
+// summed in slot order.
+constexpr int kCombineWaves = 8;
+constexpr int kMaxTopk = 64;
+
+__global__ __launch_bounds__(kCombineWaves * 64) void combine_kernel(
+    const float* __restrict__ ws, int S, int n_routes, int H, const int* route_pos,
+    const int* row_expert, const int64_t* down_svh_tab, const void* weights, int w_dtype, int topk,
+    void* out, int out_dtype) {
+    __shared__ float part[kMaxTopk][128];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nJ = H >> 7;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= T * nJ) return;
-    const int t = item / nJ, j = item % nJ;
+    const int t = blockIdx.x / nJ, j = blockIdx.x % nJ;
     const int c0 = j * 128 + lane;
-    float acc0 = 0.f, acc1 = 0.f;
-    for (int k = 0; k < topk; ++k) {
+    for (int k = wave; k < topk; k += kCombineWaves) {
         const int pos = route_pos[t * topk + k];
-        if (pos < 0) continue;
         float v0 = 0.f, v1 = 0.f;
-        for (int ss = 0; ss < S; ++ss) {
-            const float* src = ws + ((int64_t)ss * n_routes + pos) * H;
-            v0 += src[c0];
-            v1 += src[c0 + 64];
+        if (pos >= 0) {
+            sum_splits(ws + (int64_t)pos * H, (int64_t)n_routes * H, S, c0, v0, v1);
+            finish_block(v0, v1, reinterpret_cast<const uint16_t*>(down_svh_tab[row_expert[pos]]),
+                         c0, lane);
+            const int64_t wi = (int64_t)t * topk + k;
+            float w;
+            if (w_dtype == kF32)
+                w = reinterpret_cast<const float*>(weights)[wi];
+            else if (w_dtype == kF16)
+                w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wi]);
+            else
+                w = __builtin_bit_cast(float,
+                                       (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wi] << 16);
+            v0 *= w;
+            v1 *= w;
         }
-        finish_block(v0, v1, reinterpret_cast<const uint16_t*>(down_svh_tab[row_expert[pos]]), c0,
-                     lane);
-        const int64_t wi = (int64_t)t * topk + k;
-        float w;
-        if (w_dtype == kF32)
-            w = reinterpret_cast<const float*>(weights)[wi];
-        else if (w_dtype == kF16)
-            w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wi]);
-        else
-            w = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wi] << 16);
-        acc0 += w * v0;
-        acc1 += w * v1;
+        part[k][lane] = v0;
+        part[k][lane + 64] = v1;
     }
-    const int64_t o = (int64_t)t * H + c0;
-    store_out(out, out_dtype, o, acc0);
-    store_out(out, out_dtype, o + 64, acc1);
+    __syncthreads();
+    if (threadIdx.x < 128) {
+        float acc = 0.f;
+        for (int k = 0; k < topk; ++k) acc += part[k][threadIdx.x];
+        store_out(out, out_dtype, (int64_t)t * H + j * 128 + threadIdx.x, acc);
+    }
 }
 
 // ---------------------------------------------------------------------------
 // Host-side planning (shared by the workspace queries and the launches)
 // ---------------------------------------------------------------------------
 constexpr int kTargetItems = 2048;
+constexpr int kMaxSplits = 4;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -509,22 +599,23 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 inline int pick_splits(int n_hb, int base_items) {
     int best = 1;
     for (int d = 1; d <= n_hb; ++d)
-        if (n_hb % d == 0 && (int64_t)base_items * d <= kTargetItems) best = d;
+        if (n_hb % d == 0 && d <= kMaxSplits && (int64_t)base_items * d <= kTargetItems) best = d;
     return best;
 }
 
 // Hadamard blocks whose activations fit the LDS budget at once.
 inline int pick_chunk(int R_hb, int nproj, int MRB) {
-    const int per_hb = nproj * 8 * MRB * 16 * 2;  // bytes
+    (void)nproj;
+    const int per_hb = 8 * MRB * 16 * 2;  // bytes of staged activations per 128-row block
     int c = (40 * 1024) / per_hb;
     if (c < 1) c = 1;
     return c < R_hb ? c : R_hb;
 }
 
 inline size_t gemv_lds_bytes(int C_hb, int nproj, int MRB) {
-    const size_t a = (size_t)nproj * C_hb * 8 * MRB * 16 * 2;
+    const size_t a = (size_t)C_hb * 8 * MRB * 16 * 2;
     const size_t r = (size_t)nproj * MRB * 128 * 4;
-    return kWaves * kStageBytes + (a > r ? a : r);
+    return kWaves * kStageBytes + a + r;
 }
 
 struct PhasePlan {
@@ -553,9 +644,11 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
     MoePlan m;
     m.n_routes = (int)(T * topk);
     m.max_slots = (int)(m.n_routes < n_local ? m.n_routes : n_local);
-    m.MRB = (int)(T < kMaxMRB ? (T < 1 ? 1 : T) : kMaxMRB);
+    // a routing slot rarely holds more than 8 of the T rows at decode; larger
+    // slots run extra row groups (the weights are streamed once per group)
+    m.MRB = (int)(T < kMoeMRB ? (T < 1 ? 1 : T) : kMoeMRB);
     m.nproj = gateless ? 1 : 2;
-    m.gu = plan_phase((int)hidden, m.max_slots * (int)(inter / 128), m.nproj, m.MRB);
+    m.gu = plan_phase((int)hidden, m.max_slots * (int)(inter / 128) * m.nproj, 1, m.MRB);
     m.dn = plan_phase((int)inter, m.max_slots * (int)(hidden / 128), 1, m.MRB);
     size_t off = 0;
     m.off_route = off;
@@ -696,6 +789,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
                               int64_t workspace_bytes, void* stream) {
     EXL3_CHECK(T >= 1 && topk >= 1 && T * topk <= kMaxRoutes,
                "fused MoE decode supports 1 <= T*topk <= %d routes", kMaxRoutes);
+    EXL3_CHECK(topk <= kMaxTopk, "fused MoE supports topk <= %d", kMaxTopk);
     EXL3_CHECK(hidden > 0 && hidden % 128 == 0,
                "fused MoE hidden width must be a positive multiple of 128");
     EXL3_CHECK(inter > 0 && inter % 128 == 0,
@@ -773,7 +867,8 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pg.R_hb = mp.gu.R_hb;
     pg.C_hb = mp.gu.C_hb;
     pg.ws = ws_gu;
-    launch_gemv<kModeGateUp>(codebook, mp.max_slots * (int)(inter / 128) * mp.gu.S, mp.gu.lds, st, pg);
+    launch_gemv<kModeGateUp>(codebook, mp.max_slots * (int)(inter / 128) * mp.gu.S * mp.nproj,
+                             mp.gu.lds, st, pg);
     EXL3_LAUNCHED();
 
     // down: finishes gate/up while staging, raw partials [S_d][routes][hidden]
@@ -789,10 +884,9 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     launch_gemv<kModeDown>(codebook, mp.max_slots * (int)(hidden / 128) * mp.dn.S, mp.dn.lds, st, pd);
     EXL3_LAUNCHED();
 
-    const int items = (int)(T * (hidden / 128));
-    combine_kernel<<<(items + 3) / 4, 256, 0, st>>>(ws_d, mp.dn.S, mp.n_routes, (int)hidden,
-                                                    ro.route_pos, ro.row_expert, down_svh, weights,
-                                                    w_dtype, (int)T, (int)topk, out, out_dtype);
+    combine_kernel<<<(int)(T * (hidden / 128)), kCombineWaves * 64, 0, st>>>(
+        ws_d, mp.dn.S, mp.n_routes, (int)hidden, ro.route_pos, ro.row_expert, down_svh, weights,
+        w_dtype, (int)topk, out, out_dtype);
     EXL3_LAUNCHED();
     return kOk;
 }

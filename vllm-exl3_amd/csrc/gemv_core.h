@@ -37,7 +37,7 @@ enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kDepth = 4;          // tile rows in flight per wave
+constexpr int kDepth = 8;          // tile rows in flight per wave
 constexpr int kStageBytes = 1024;  // one tile row of 8 tiles at K <= 4
 
 struct GemvParams {
@@ -130,33 +130,38 @@ __device__ __forceinline__ LaneWords lane_words(int lane) {
     return w;
 }
 
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
 // Decode the lane's four weights of one tile into MFMA B registers (each a
-// (lo, hi) fp16 pair whose sum is the weight).
+// (lo, hi) fp16 pair whose sum is the weight).  Per weight, for the two
+// "sum of halves" codebooks: one shift (none for the last window), then
+// x*C mod 2^32 = x*C_lo + ((x*C_hi) << 16) as v_mad_u32_u16 (the 16-bit
+// multiplier reads only the window's low 16 bits, so no mask is needed; the
+// 3INST addend folds in) plus one v_pk_mad_u16 whose low lane adds 0, and one
+// v_bitop3 for the mask/xor: four VALU ops per weight.
 template <int K, int CB>
 __device__ __forceinline__ void decode4(uint32_t hi, uint32_t lo, uint32_t shift, uint32_t b[4]) {
     const uint32_t s = __builtin_amdgcn_alignbit(hi, lo, shift);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t w = __builtin_amdgcn_ubfe(s, (3 - i) * K, 16);
+        const uint32_t sh = s >> ((3 - i) * K);
         if constexpr (CB == kCbMul1) {
-            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(w));  // (value, +0)
+            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(sh & 0xFFFFu));  // (value, +0)
         } else {
-            // x*C mod 2^32 = x*C_lo + (x*C_hi << 16): the low product on the
-            // full-rate 24-bit multiplier (the 3INST addend folded in), the
-            // high half with one packed 16-bit mad (lo lane adds 0).  Written
-            // as asm because the compiler otherwise re-fuses the pieces into a
-            // quarter-rate v_mul_lo_u32.
             constexpr uint32_t C = (CB == kCb3Inst) ? 89226354u : 0xCBAC1FEDu;
-            constexpr uint32_t A = (CB == kCb3Inst) ? 64248484u : 0u;
-            const uint32_t c_lo = C & 0xFFFFu, c_hi = C & 0xFFFF0000u;
-            uint32_t lo_prod, x;
-            if constexpr (A != 0) {
-                asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(lo_prod) : "v"(w), "s"(c_lo), "v"(A));
+            const uint32_t c_lo = C & 0xFFFFu;
+            uint32_t lo_prod;
+            if constexpr (CB == kCb3Inst) {
+                const uint32_t add = 64248484u;
+                asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(lo_prod) : "v"(sh), "s"(c_lo), "v"(add));
             } else {
-                asm("v_mul_u32_u24 %0, %1, %2" : "=v"(lo_prod) : "v"(w), "s"(c_lo));
+                asm("v_mad_u32_u16 %0, %1, %2, 0" : "=v"(lo_prod) : "v"(sh), "s"(c_lo));
             }
-            asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel_hi:[0,1,1]" : "=v"(x) : "v"(w), "s"(c_hi), "v"(lo_prod));
-            b[i] = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+            const unsigned short w16 = (unsigned short)sh;
+            const u16x2_t xv = {w16, w16};
+            const u16x2_t cv = {(unsigned short)0, (unsigned short)(C >> 16)};
+            const u16x2_t r = xv * cv + __builtin_bit_cast(u16x2_t, lo_prod);
+            b[i] = (__builtin_bit_cast(uint32_t, r) & 0x8FFF8FFFu) ^ 0x3B603B60u;
         }
     }
 }
