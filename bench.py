@@ -1,0 +1,199 @@
+#!/usr/bin/env python3
+"""Benchmark of the EXL3 routed-expert decode path on one MI355X.
+
+Workload: one routed-MoE decode layer, 64 experts, top-8,
+hidden 2048, per-expert intermediate 1536, fused gate/up + SiLU + down, K3
+3INST trellis weights (seeded random bits, random suh/svh), bf16 activations
+N(0,1), softmax top-8 routing.  A step is one layer forward for a batch of T
+tokens; the headline is T = 16, with T = 1 and 4 reported alongside.
+
+value = packed expert bytes touched per step (distinct routed experts x
+3,560,448 B + activations) / time per step, inputs resident in HBM.
+roofline = the dominant kernel (the gate/up GEMV) timed live with HIP events
+on its launch stream, against the 8 TB/s HBM peak.
+cpu_baseline = the CPU oracle's eager per-expert loop (single-threaded dequant
+as the reference's host decoder, torch fp32 matmul on all host threads) on a
+time-bounded sample of the same routed experts.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (ROOT / "vllm-exl3_amd", ROOT / "oracle"):
+    sys.path.insert(0, str(p))
+
+E, H, I, TOPK, K, CB = 64, 2048, 1536, 8, 3, 0
+EXPERT_BYTES = 3 * H * I * K // 8 + 2 * 3 * (H + I)  # trellis + suh/svh of 3 projections
+HBM_PEAK_GBS = 8000.0
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def run_batch(C, S, torch, layer, T, steps, warmup, dev, PhaseTimer):
+    x = torch.from_numpy(S.activations(10 + T, T, H)).to(dev).bfloat16()
+    ids_np, w_np = S.softmax_topk(20 + T, T, E, TOPK)
+    U = len(set(ids_np.ravel().tolist()))
+    ids = torch.from_numpy(ids_np).to(dev)
+    w = torch.from_numpy(w_np).to(dev)
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+
+    def step():
+        C.moe_forward(x, ids, w, layer, E, I, K=(K, K, K), codebook=CB, out=out)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with PhaseTimer(max_calls=steps) as pt:
+        start.record()
+        for _ in range(steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    step_bytes = U * EXPERT_BYTES + 2 * T * H + 4 * T * H
+    gu_bytes = U * 2 * (H * I * K // 8 + 2 * (H + I)) + 2 * T * H  # gate+up trellis, scales, x
+    gu_ms = pt.mean_ms(1)
+    return {
+        "T": T, "distinct_experts": U, "us_per_step": ms * 1e3, "gbs": step_bytes / (ms * 1e-3) / 1e9,
+        "phase_us": {n: pt.mean_ms(i) * 1e3 for i, n in enumerate(("route", "gate_up", "down", "combine"))},
+        "gate_up_bytes": gu_bytes, "gate_up_gbs": gu_bytes / (gu_ms * 1e-3) / 1e9,
+        "ids": ids_np, "x": x,
+    }
+
+
+def cpu_baseline(S, O, torch, experts, ids_np, x, budget_s=12.0):
+    """The reference's CPU eager path on the routed experts of the batch, in
+    routing order, until the time budget is spent: per expert, the host
+    dequant (single-threaded, as csrc/bindings.cpp:15-100) of gate/up/down and
+    the fp32 matmuls of the per-expert loop (src/vllm_exl3/exl3.py:2357-2413)."""
+    import numpy as np
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    xf = x.float().cpu().to(torch.float16).float()
+    order = []
+    for e in ids_np.ravel().tolist():
+        if e not in order:
+            order.append(e)
+    done, nbytes, t_dq, t_mm = 0, 0, 0.0, 0.0
+    t0 = time.perf_counter()
+    for e in order:
+        pk = experts[e]
+        t1 = time.perf_counter()
+        w = {p: torch.from_numpy(O.dequant(pk[p]["trellis"], pk[p]["suh"], pk[p]["svh"], K, CB)
+                                 .astype(np.float32)) for p in ("gate", "up", "down")}
+        t2 = time.perf_counter()
+        rows = torch.from_numpy(np.nonzero((ids_np == e).any(axis=1))[0])
+        h = xf.index_select(0, rows)
+        g = (h @ w["gate"]).half().float()
+        u = (h @ w["up"]).half().float()
+        a = (torch.nn.functional.silu(g) * u).half().float()
+        _ = a @ w["down"]
+        t3 = time.perf_counter()
+        t_dq += t2 - t1
+        t_mm += t3 - t2
+        done += 1
+        nbytes += EXPERT_BYTES
+        if time.perf_counter() - t0 > budget_s:
+            break
+    total = t_dq + t_mm
+    return {
+        "value": nbytes / total / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{done} of {len(order)} routed experts of the T={ids_np.shape[0]} batch "
+                   f"(dequant of gate/up/down single-threaded {t_dq:.2f} s + fp32 matmul "
+                   f"{t_mm:.3f} s on {torch.get_num_threads()} threads; {cpu_model()}, "
+                   f"os.cpu_count()={os.cpu_count()})"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batches", default="1,4,16",
+                    help="decode batch sizes T to run; the headline is the largest")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(the routed-expert layer shards by expert; see DESIGN.md)", file=sys.stderr)
+        return 2
+    import torch
+
+    from vllm_exl3_amd import synthetic as S
+    from vllm_exl3_amd import vllm_exl3_c as C
+    from vllm_exl3_amd.profiling import PhaseTimer
+
+    dev = torch.device("cuda", 0)
+    experts = S.moe_layer(1, E, H, I, K)
+    layer = S.to_device(experts, dev)
+    batches = sorted({int(b) for b in args.batches.split(",")})
+    results = {T: run_batch(C, S, torch, layer, T, args.steps, args.warmup, dev, PhaseTimer)
+               for T in batches}
+    T_head = batches[-1]
+    head = results[T_head]
+    line = {
+        "metric": "MoE-layer decode µs + packed-weight HBM GB/s; prefill TFLOP/s (EXL3 K2–K4)",
+        "value": round(head["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_step"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"C1 routed-MoE decode layer, E64 top-8, H2048 I1536, K3 3INST, bf16 x, T={T_head}",
+            "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "K": K, "codebook": "3INST",
+            "tokens": T_head, "distinct_experts": head["distinct_experts"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_kernel<3INST, gate/up>",
+            "achieved": round(head["gate_up_gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(head["gate_up_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": head["gate_up_bytes"],
+            "us_per_launch": round(head["phase_us"]["gate_up"], 3),
+        },
+        "per_batch": {
+            f"T={T}": {"us_per_step": round(r["us_per_step"], 2), "GB/s": round(r["gbs"], 1),
+                       "distinct_experts": r["distinct_experts"],
+                       "phase_us": {k: round(v, 2) for k, v in r["phase_us"].items()}}
+            for T, r in results.items()
+        },
+    }
+    if not args.no_cpu_baseline:
+        import oracle as O
+
+        line["cpu_baseline"] = cpu_baseline(S, O, torch, experts, head["ids"], head["x"])
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -106,6 +106,18 @@ int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hidden, int6
                      void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Instrumentation (no counterpart in the reference; used by the benchmark to
+ * time individual kernels on their launch stream).  Between begin and end,
+ * every instrumented call records HIP events at its phase boundaries:
+ *   exl3_moe_forward: 0 route | 1 gate/up GEMV | 2 down GEMV | 3 combine
+ *   exl3_gemm:        0 GEMV | 1 split finish (when split)
+ * Recording never synchronises.  exl3_profile_end waits for the events and
+ * writes, per phase, the summed elapsed milliseconds over the recorded calls
+ * (at most max_calls are recorded).  Not thread-safe. */
+int exl3_profile_begin(int max_calls);
+int exl3_profile_end(double* phase_ms, int max_phases, int* n_calls, int* n_phases);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,7 @@
 //                (rotation x svh) and sum w * d in slot order
 //                (csrc/p2b_moe.cu:1976-2008): deterministic, no atomics.
 #include "gemv_core.h"
+#include "profile.h"
 
 #include <cmath>
 
@@ -758,13 +759,17 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     p.n_rows_ws = (int)m;
     p.ws = reinterpret_cast<float*>(workspace);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    profile_begin_call();
+    profile_mark(0, st);
     launch_gemv<kModeLinear>(codebook, (int)(out_f / 128) * lp.ph.S, lp.ph.lds, st, p);
     EXL3_LAUNCHED();
+    profile_mark(1, st);
     if (lp.ph.S > 1) {
         const int items = (int)(m * (out_f / 128));
         linear_finish_kernel<<<(items + 3) / 4, 256, 0, st>>>(p.ws, lp.ph.S, (int)m, (int)out_f, svh,
                                                               out, out_dtype);
         EXL3_LAUNCHED();
+        profile_mark(2, st);
     }
     return kOk;
 }
@@ -820,6 +825,8 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
 
+    profile_begin_call();
+    profile_mark(0, st);
     RouteOut ro;
     int* rbase = reinterpret_cast<int*>(ws + mp.off_route);
     ro.n_active = rbase;
@@ -867,6 +874,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pg.R_hb = mp.gu.R_hb;
     pg.C_hb = mp.gu.C_hb;
     pg.ws = ws_gu;
+    profile_mark(1, st);
     launch_gemv<kModeGateUp>(codebook, mp.max_slots * (int)(inter / 128) * mp.gu.S * mp.nproj,
                              mp.gu.lds, st, pg);
     EXL3_LAUNCHED();
@@ -881,12 +889,15 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pd.R_hb = mp.dn.R_hb;
     pd.C_hb = mp.dn.C_hb;
     pd.ws = ws_d;
+    profile_mark(2, st);
     launch_gemv<kModeDown>(codebook, mp.max_slots * (int)(hidden / 128) * mp.dn.S, mp.dn.lds, st, pd);
     EXL3_LAUNCHED();
 
+    profile_mark(3, st);
     combine_kernel<<<(int)(T * (hidden / 128)), kCombineWaves * 64, 0, st>>>(
         ws_d, mp.dn.S, mp.n_routes, (int)hidden, ro.route_pos, ro.row_expert, down_svh, weights,
         w_dtype, (int)topk, out, out_dtype);
     EXL3_LAUNCHED();
+    profile_mark(4, st);
     return kOk;
 }
