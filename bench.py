@@ -33,6 +33,10 @@ for p in (ROOT / "vllm-exl3_amd", ROOT / "oracle"):
 E, H, I, TOPK, K, CB = 64, 2048, 1536, 8, 3, 0
 EXPERT_BYTES = 3 * H * I * K // 8 + 2 * 3 * (H + I)  # trellis + suh/svh of 3 projections
 HBM_PEAK_GBS = 8000.0
+# HBM bytes of one gate/up launch at T=16 (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000,
+# factors from a 256 MiB copy), from profiles/moe_decode_c1_t16.md; re-measured
+# with rocprofv3 --pmc whenever the kernel changes.
+GATE_UP_TRAFFIC_T16 = 144_208_486 + 1_572_864
 
 
 def cpu_model() -> str:
@@ -132,10 +136,24 @@ def main() -> int:
     ap.add_argument("--batches", default="1,4,16",
                     help="decode batch sizes T to run; the headline is the largest")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (the known-size "
+                         "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+
+        n = args.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 5}), flush=True)
+        return 0
     if args.gpus != 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
-              "(the routed-expert layer shards by expert; see DESIGN.md)", file=sys.stderr)
+              "(the routed-expert layer would shard by expert; no collectives are built)", file=sys.stderr)
         return 2
     import torch
 
@@ -176,7 +194,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(head["gate_up_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GATE_UP_TRAFFIC_T16 if T_head == 16 else None,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/moe_decode_c1_t16.md",
             "bytes_per_launch": head["gate_up_bytes"],
             "us_per_launch": round(head["phase_us"]["gate_up"], 3),
         },
