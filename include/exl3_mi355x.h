@@ -107,11 +107,62 @@ int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hidden, int6
                      void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Prefill ("fat") GEMM: out[M, N] = had128(A x Wq) * svh in fp32, where A is
+ * fp16 [M, K_in] row-major and already input-rotated by the caller (x * suh
+ * then the 128-block Hadamard), Wq the decoded trellis tiles.  K in {2,3,4},
+ * any codebook; K_in and N multiples of 128.  Tiles of 256 rows x 256 columns
+ * decode the packed bits once into LDS and feed v_mfma_f32_16x16x32_f16.
+ * Replaces vllm_exl3_c.exl3_fat_gemm (csrc/bindings.cpp:259-261,
+ * csrc/exl3_fat_gemm.cu:65-197, 277-287; K4 MCG only there). */
+int exl3_fat_gemm(const uint16_t* a, int64_t M, const int16_t* trellis, int64_t tiles_k,
+                  int64_t tiles_n, int64_t K, int codebook, const uint16_t* svh, float* out,
+                  void* stream);
+
+/* Scatter variant: out[token_idx[r], :] += route_weight[r] * row r of the
+ * product (fp32 atomics; rows of one call are expected to carry distinct
+ * tokens, as the reference assumes; rows whose token is outside
+ * [0, out_rows) are dropped).  Needs a workspace of
+ * exl3_fat_gemm_workspace_size(M, N, 1) bytes.
+ * Replaces vllm_exl3_c.exl3_fat_gemm_scatter (csrc/bindings.cpp:262-265,
+ * csrc/exl3_fat_gemm.cu:289-305). */
+int64_t exl3_fat_gemm_workspace_size(int64_t M, int64_t out_features, int scatter);
+int exl3_fat_gemm_scatter(const uint16_t* a, int64_t M, const int16_t* trellis, int64_t tiles_k,
+                          int64_t tiles_n, int64_t K, int codebook, const uint16_t* svh,
+                          const int64_t* token_idx, const uint16_t* route_weight, float* out,
+                          int64_t out_rows, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Routed-expert MoE forward for prefill-sized batches, same arguments and
+ * results as exl3_moe_forward (n_local <= 1023): device routing sort ->
+ * gate/up input rotation per routed row -> grouped fat GEMM (gate, up) ->
+ * activation + down input rotation -> grouped fat GEMM (down) -> per-token
+ * combine in slot order (deterministic).
+ * Replaces the prefill side of the reference's routed-expert dispatch:
+ * apply_exl3_fused_moe / apply_exl3_batched_fat (src/vllm_exl3/exl3.py:
+ * 2981-3599) with ExLlamaV3 exl3_moe / exl3_moe_mixedk and the per-expert
+ * exl3_fat_gemm{,_scatter} host loop. */
+int64_t exl3_moe_prefill_workspace_size(int64_t T, int64_t topk, int64_t n_local, int64_t hidden,
+                                        int64_t inter, int gateless);
+int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hidden, int64_t inter,
+                     const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                     const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                     const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                     int64_t n_local, const int8_t* k_gate, const int8_t* k_up, const int8_t* k_down,
+                     int64_t K_gate, int64_t K_up, int64_t K_down, int codebook, int gateless,
+                     int act, float swiglu_limit, const void* ids, int ids_dtype,
+                     const void* weights, int w_dtype, int64_t topk, const int32_t* n_valid,
+                     void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+/* ---------------------------------------------------------------------------
  * Instrumentation (no counterpart in the reference; used by the benchmark to
  * time individual kernels on their launch stream).  Between begin and end,
  * every instrumented call records HIP events at its phase boundaries:
  *   exl3_moe_forward: 0 route | 1 gate/up GEMV | 2 down GEMV | 3 combine
  *   exl3_gemm:        0 GEMV | 1 split finish (when split)
+ *   exl3_moe_prefill: 0 route | 1 input rotation | 2 gate/up GEMMs | 3 activation
+ *                     | 4 down GEMM | 5 combine
+ *   exl3_fat_gemm{,_scatter}: 0 GEMM | 1 output rotation (+ scatter)
  * Recording never synchronises.  exl3_profile_end waits for the events and
  * writes, per phase, the summed elapsed milliseconds over the recorded calls
  * (at most max_calls are recorded).  Not thread-safe. */

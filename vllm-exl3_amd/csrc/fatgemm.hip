@@ -1,0 +1,805 @@
+// Prefill ("fat") EXL3 GEMM and the routed-expert prefill executor on gfx950.
+//
+// Replaces the reference's exl3_fat_gemm / exl3_fat_gemm_scatter
+// (csrc/exl3_fat_gemm.cu:65-305, K4 MCG only there) and the prefill side of
+// the routed-expert dispatch (apply_exl3_fused_moe + apply_exl3_batched_fat,
+// src/vllm_exl3/exl3.py:2981-3599, which sort on the host and loop over fat
+// experts in Python).
+//
+// GEMM tile: one 256-thread workgroup (4 wave64s in a 2x2 grid) owns 256 rows
+// x 256 output columns of one expert; each wave accumulates 128x128 with
+// v_mfma_f32_16x16x32_f16.  Per 32-deep k-step, the packed trellis of the
+// step (2 tile rows x 16 tiles) is decoded ONCE by the workgroup into an LDS
+// B tile of real fp16 weights (the codebook's two halves summed with one
+// packed fp16 add, which rounds the exact sum once like the reference's
+// decoder) and reused by every row of the tile.  Thread t decodes the 32
+// weights of one 8-index group of one tile: for such a group the window
+// offsets inside the group's K+1 words are compile-time constants, so the
+// decode needs no dynamic register indexing.  The four 16-byte units it
+// produces are eight consecutive k of one column: exactly one MFMA B-operand
+// lane fragment, stored with one ds_write_b128.
+//
+// Pipeline (one barrier per k-step): global loads of A rows and packed bits
+// run two k-steps ahead (3 LDS buffers), the decode of step s+1 is issued in
+// the same basic block as the MFMAs of step s so the scheduler can overlap
+// VALU decode with matrix-core work.  Waves whose 128-row slice holds no rows
+// of the expert skip their MFMAs but still share the decode.
+//
+// The output rotation is not done in the GEMM epilogue: the GEMM stores
+// Z / sqrt(128) (Z = A x Wq) and the consumer kernel - the activation kernel,
+// the combine, or the drop-in's output pass - applies the 128-point Hadamard
+// and svh where it is otherwise memory-bound.
+#include "exl3_common.h"
+#include "gemv_core.h"
+#include "profile.h"
+#include "route.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace exl3 {
+namespace {
+
+constexpr int kFatThreads = 256;
+constexpr int kTM = 256;        // rows per tile
+constexpr int kTN = 256;        // output columns per tile
+constexpr int kTK = 32;         // k per step (two tile rows)
+constexpr int kLdk = 40;        // fp16 per LDS row of A / B (32 + 8 pad)
+constexpr int kABytes = kTM * kLdk * 2;
+constexpr int kBBytes = kTN * kLdk * 2;
+constexpr int kTBytesMax = 1024 * 4;  // packed bytes per k-step at K <= 4
+constexpr int kFatLds = 3 * kABytes + 2 * kBBytes + 3 * kTBytesMax;
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const v4u* gv4p;
+
+struct FatParams {
+    // A: fp16 rows; row r of the tile is a + (a_row) * lda
+    const uint16_t* a;
+    int64_t lda;
+    // weights
+    const uint8_t* trellis;       // single problem
+    const int64_t* trellis_tab;   // grouped: per expert
+    const int8_t* ktab;           // grouped: per-expert K (nullable)
+    int kuni;
+    int K_in, N;
+    // output: Z * out_scale, fp16 or fp32, row stride ldo
+    void* out;
+    int out_f32;
+    int64_t ldo;
+    float out_scale;
+    // tiles
+    int grouped;
+    int M;                        // single problem rows
+    const int* n_mtiles;
+    const int* mt_slot;
+    const int* mt_row0;
+    const int* slot_expert;
+    const int* slot_start;
+    const int* slot_rows;
+    int n_ntiles;
+    int n_tiles;                  // max_mtiles * n_ntiles (grid before XCD rounding)
+};
+
+// Decoded (lo, hi) half pair of one window for the sum-of-halves codebooks,
+// masked; the weight is half(lo) + half(hi).
+template <int CB>
+__device__ __forceinline__ uint32_t fat_pair(uint32_t w) {
+    constexpr uint32_t C = (CB == kCb3Inst) ? 89226354u : 0xCBAC1FEDu;
+    const uint32_t c_lo = C & 0xFFFFu;
+    uint32_t lo_prod;
+    if constexpr (CB == kCb3Inst) {
+        const uint32_t add = 64248484u;
+        asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(lo_prod) : "v"(w), "s"(c_lo), "v"(add));
+    } else {
+        asm("v_mad_u32_u16 %0, %1, %2, 0" : "=v"(lo_prod) : "v"(w), "s"(c_lo));
+    }
+    const unsigned short w16 = (unsigned short)w;
+    const u16x2_t xv = {w16, w16};
+    const u16x2_t cv = {(unsigned short)0, (unsigned short)(C >> 16)};
+    const u16x2_t r = xv * cv + __builtin_bit_cast(u16x2_t, lo_prod);
+    return (__builtin_bit_cast(uint32_t, r) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+}
+
+// Two weights (index i, index i+1 of a tile) as a packed fp16 pair from the
+// 32 stream bits ending at the end of window i+1.
+template <int K, int CB>
+__device__ __forceinline__ uint32_t decode_pair(uint32_t s) {
+    const uint32_t wa = s >> K;  // window of index i
+    const uint32_t wb = s;       // window of index i + 1 (low 16 bits)
+    if constexpr (CB == kCbMul1) {
+        const uint32_t ha = half_to_bits(decode_weight<kCbMul1>(wa & 0xFFFFu));
+        const uint32_t hb = half_to_bits(decode_weight<kCbMul1>(wb & 0xFFFFu));
+        return ha | (hb << 16);
+    } else {
+        const uint32_t xa = fat_pair<CB>(wa);
+        const uint32_t xb = fat_pair<CB>(wb);
+        // lows = (xa.lo, xb.lo), highs = (xa.hi, xb.hi); weights = lows + highs
+        const uint32_t lows = __builtin_amdgcn_perm(xb, xa, 0x05040100u);
+        const uint32_t highs = __builtin_amdgcn_perm(xb, xa, 0x07060302u);
+        const half2_t w = __builtin_bit_cast(half2_t, lows) + __builtin_bit_cast(half2_t, highs);
+        return __builtin_bit_cast(uint32_t, w);
+    }
+}
+
+// Word offset (relative to the group's first word) and funnel shift of pair
+// p of unit (b1, b2): the pair's 32 stream bits end at
+// E = (2 b1 + 4 b2 + 2 + 8 p) K + 32 bits after the group's first word.
+template <int K>
+struct PairGeom {
+    static constexpr int end(int b1, int b2, int p) { return (2 * b1 + 4 * b2 + 2 + 8 * p) * K + 32; }
+    static constexpr int rel(int b1, int b2, int p) { return (end(b1, b2, p) - 1) >> 5; }
+    static constexpr int shift(int b1, int b2, int p) { return 32 * (rel(b1, b2, p) + 1) - end(b1, b2, p); }
+};
+
+// Decode the 32 weights of group g of one staged tile into four B units.
+template <int K, int CB>
+__device__ __forceinline__ void decode_group(const uint8_t* tile, int g, uint16_t* bl, int n_base,
+                                             int k_base) {
+    constexpr int n32 = 8 * K;
+    constexpr int NW = K + 1;
+    uint32_t w[NW];
+    const uint32_t* tw = reinterpret_cast<const uint32_t*>(tile);
+    const int F = g * K - 1;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int idx = F + j;
+        w[j] = tw[idx < 0 ? idx + n32 : idx];
+    }
+#pragma unroll
+    for (int b1 = 0; b1 < 2; ++b1)
+#pragma unroll
+        for (int b2 = 0; b2 < 2; ++b2) {
+            v4u u;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int rel = PairGeom<K>::rel(b1, b2, p);
+                const uint32_t s =
+                    __builtin_amdgcn_alignbit(w[rel - 1], w[rel], PairGeom<K>::shift(b1, b2, p));
+                u[p] = decode_pair<K, CB>(s);
+            }
+            const int n = n_base + g + 8 * b2;
+            *reinterpret_cast<v4u*>(bl + n * kLdk + k_base + 8 * b1) = u;
+        }
+}
+
+template <int CB, int K>
+__device__ __forceinline__ void fat_tile(const FatParams& p, uint8_t* lds, const uint8_t* trellis,
+                                         int64_t a_row0, int rows_valid, int64_t out_row0, int nt) {
+    uint16_t* Abuf = reinterpret_cast<uint16_t*>(lds);
+    uint16_t* Bbuf = reinterpret_cast<uint16_t*>(lds + 3 * kABytes);
+    uint8_t* Tbuf = lds + 3 * kABytes + 2 * kBBytes;
+    constexpr int tile_bytes = 32 * K;
+    constexpr int tbytes = 32 * tile_bytes;  // 2 tile rows x 16 tiles
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tiles_n = p.N >> 4;
+    const int n_cols = min(kTN, p.N - nt * kTN);      // 128 or 256
+    const int tcols = n_cols >> 4;                      // valid tile columns (8 or 16)
+    const int nsteps = p.K_in / kTK;
+
+    // ---- global loads of one k-step into registers
+    v4u ga[4];
+    v4u gt;
+    const int a_chunk = tid & 3;
+    auto load_step = [&](int s) {
+        const int k0 = s * kTK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int r = (tid >> 2) + 64 * j;
+            r = min(r, rows_valid - 1);
+            ga[j] = __builtin_nontemporal_load(
+                (gv4p)(p.a + (a_row0 + r) * p.lda + k0 + a_chunk * 8));
+        }
+        const int off = tid * 16;
+        const int seg = off / (16 * tile_bytes);
+        const int in_seg = off - seg * 16 * tile_bytes;
+        if (off < tbytes && in_seg < tcols * tile_bytes) {
+            const uint8_t* src = trellis +
+                                 ((size_t)(2 * s + seg) * tiles_n + (size_t)nt * 16) * tile_bytes +
+                                 in_seg;
+            gt = __builtin_nontemporal_load((gv4p)src);
+        }
+    };
+    auto store_step = [&](int s) {
+        uint16_t* A = Abuf + (s % 3) * (kABytes / 2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = (tid >> 2) + 64 * j;
+            *reinterpret_cast<v4u*>(A + r * kLdk + a_chunk * 8) = ga[j];
+        }
+        const int off = tid * 16;
+        const int seg = off / (16 * tile_bytes);
+        const int in_seg = off - seg * 16 * tile_bytes;
+        if (off < tbytes && in_seg < tcols * tile_bytes)
+            *reinterpret_cast<v4u*>(Tbuf + (s % 3) * kTBytesMax + off) = gt;
+    };
+    // ---- decode of one k-step: thread -> (tile row, tile column, group)
+    const int d_sel = tid >> 7, d_col = (tid >> 3) & 15, d_g = tid & 7;
+    auto decode_step = [&](int s) {
+        if (d_col < tcols) {
+            const uint8_t* tile = Tbuf + (s % 3) * kTBytesMax + (d_sel * 16 + d_col) * tile_bytes;
+            decode_group<K, CB>(tile, d_g, Bbuf + (s & 1) * (kBBytes / 2), d_col * 16, d_sel * 16);
+        }
+    };
+
+    float4_t acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int m_rows = rows_valid - wm * 128;
+    const int mf_valid = m_rows <= 0 ? 0 : min(8, (m_rows + 15) >> 4);
+    const bool wave_on = (wn * 128 < n_cols) && mf_valid > 0;
+
+    // ---- prologue: steps 0 and 1 staged, step 0 decoded
+    load_step(0);
+    store_step(0);
+    if (nsteps > 1) {
+        load_step(1);
+        store_step(1);
+    }
+    __syncthreads();
+    decode_step(0);
+    __syncthreads();
+
+    const int frag_k = 8 * (lane >> 4);
+    for (int s = 0; s < nsteps; ++s) {
+        const bool pre = s + 2 < nsteps;
+        if (pre) load_step(s + 2);
+        if (s + 1 < nsteps) decode_step(s + 1);
+        if (wave_on) {
+            const uint16_t* A = Abuf + (s % 3) * (kABytes / 2);
+            const uint16_t* B = Bbuf + (s & 1) * (kBBytes / 2);
+            half8_t bf[8];
+#pragma unroll
+            for (int nf = 0; nf < 8; ++nf)
+                bf[nf] = *reinterpret_cast<const half8_t*>(
+                    B + (wn * 128 + nf * 16 + (lane & 15)) * kLdk + frag_k);
+#pragma unroll
+            for (int mf = 0; mf < 8; ++mf) {
+                if (mf < mf_valid) {
+                    const half8_t af = *reinterpret_cast<const half8_t*>(
+                        A + (wm * 128 + mf * 16 + (lane & 15)) * kLdk + frag_k);
+#pragma unroll
+                    for (int nf = 0; nf < 8; ++nf)
+                        acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nf], acc[mf][nf],
+                                                                             0, 0, 0);
+                }
+            }
+        }
+        if (pre) store_step(s + 2);
+        __syncthreads();
+    }
+
+    // ---- epilogue: Z * out_scale
+    if (!wave_on) return;
+    const int col0 = nt * kTN + wn * 128 + (lane & 15);
+#pragma unroll
+    for (int mf = 0; mf < 8; ++mf) {
+        if (mf < mf_valid) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = wm * 128 + mf * 16 + 4 * (lane >> 4) + i;
+                if (r < rows_valid) {
+                    const int64_t o = (out_row0 + r) * p.ldo + col0;
+#pragma unroll
+                    for (int nf = 0; nf < 8; ++nf) {
+                        const float v = acc[mf][nf][i] * p.out_scale;
+                        if (p.out_f32)
+                            reinterpret_cast<float*>(p.out)[o + nf * 16] = v;
+                        else
+                            reinterpret_cast<uint16_t*>(p.out)[o + nf * 16] = half_to_bits((half_t)v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int CB>
+__global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void fat_gemm_kernel(
+    FatParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    // XCD-aware order: consecutive logical tiles (the N tiles of one row tile,
+    // which share their A rows) land on the same XCD and its L2.
+    const int G = p.n_tiles;
+    const int per = (G + 7) >> 3;
+    const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (logical >= G) return;
+    const int mt = logical / p.n_ntiles, nt = logical % p.n_ntiles;
+    int64_t a_row0, out_row0;
+    int rows_valid, K;
+    const uint8_t* trellis;
+    if (p.grouped) {
+        if (mt >= *p.n_mtiles) return;
+        const int slot = p.mt_slot[mt];
+        const int row0 = p.mt_row0[mt];
+        const int e = p.slot_expert[slot];
+        a_row0 = (int64_t)p.slot_start[slot] + row0;
+        out_row0 = a_row0;
+        rows_valid = min(kTM, p.slot_rows[slot] - row0);
+        trellis = reinterpret_cast<const uint8_t*>(p.trellis_tab[e]);
+        K = p.ktab ? (int)p.ktab[e] : p.kuni;
+    } else {
+        a_row0 = (int64_t)mt * kTM;
+        out_row0 = a_row0;
+        rows_valid = min(kTM, p.M - mt * kTM);
+        trellis = p.trellis;
+        K = p.kuni;
+    }
+    switch (K) {
+        case 2: fat_tile<CB, 2>(p, lds, trellis, a_row0, rows_valid, out_row0, nt); break;
+        case 3: fat_tile<CB, 3>(p, lds, trellis, a_row0, rows_valid, out_row0, nt); break;
+        case 4: fat_tile<CB, 4>(p, lds, trellis, a_row0, rows_valid, out_row0, nt); break;
+        default: break;  // rejected on the host
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 128-point butterfly over values held as adjacent pairs: lane l holds
+// elements 2l and 2l+1.  Unnormalised.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void had128_pair(float& a, float& b, int lane) {
+    const float s = a + b, d = a - b;
+    a = s;
+    b = d;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float pa = __shfl_xor(a, m, 64);
+        const float pb = __shfl_xor(b, m, 64);
+        if (lane & m) {
+            a = pa - a;
+            b = pb - b;
+        } else {
+            a = a + pa;
+            b = b + pb;
+        }
+    }
+}
+
+__device__ __forceinline__ float h2f(const uint16_t* p, int64_t i) { return (float)bits_to_half(p[i]); }
+
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+    return (uint32_t)half_to_bits(f32_to_f16_rne(a)) | ((uint32_t)half_to_bits(f32_to_f16_rne(b)) << 16);
+}
+
+// Gate/up input rotation of every sorted route row: A_q[row] =
+// fp16(had128(fp16(x[token]) * suh_q[expert]) / sqrt(128)) for q in gate, up.
+// One wave per (row, 128-column block).
+__global__ __launch_bounds__(256) void rotate_in_kernel(const void* x, int x_dtype, int64_t x_stride,
+                                                        int H, const int* n_sorted,
+                                                        const int* row_token, const int* row_expert,
+                                                        const int64_t* suh_g, const int64_t* suh_u,
+                                                        int nproj, uint16_t* a_g, uint16_t* a_u,
+                                                        int64_t n_units) {
+    const int lane = threadIdx.x & 63;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= n_units) return;
+    const int nb = H >> 7;
+    const int row = (int)(unit / nb), j = (int)(unit % nb);
+    if (row >= *n_sorted) return;
+    const int64_t tok = row_token[row];
+    const int e = row_expert[row];
+    const int c = j * 128 + 2 * lane;
+    const float x0 = load_act(x, x_dtype, tok * x_stride + c);
+    const float x1 = load_act(x, x_dtype, tok * x_stride + c + 1);
+    for (int q = 0; q < nproj; ++q) {
+        const uint16_t* su = reinterpret_cast<const uint16_t*>(q ? suh_u[e] : suh_g[e]);
+        float a = x0 * h2f(su, c), b = x1 * h2f(su, c + 1);
+        had128_pair(a, b, lane);
+        uint16_t* dst = q ? a_u : a_g;
+        *reinterpret_cast<uint32_t*>(dst + (int64_t)row * H + c) = pack_f16(a * kHadNorm, b * kHadNorm);
+    }
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+
+__device__ __forceinline__ float activate(float g, float u, int act, float limit) {
+    if (act == kActRelu2) {
+        if (limit > 0.0f) u = fminf(fmaxf(u, -limit), limit);
+        const float r = fmaxf(u, 0.0f);
+        return r * r;
+    }
+    if (limit > 0.0f) {
+        g = fminf(g, limit);
+        u = fminf(fmaxf(u, -limit), limit);
+    }
+    if (act == kActSwigluOai) return (u + 1.0f) * g * (1.0f / (1.0f + __expf(-1.702f * g)));
+    return silu_f(g) * u;
+}
+
+// Finish gate/up and build the down input: for each sorted row and 128-block
+// of the intermediate dimension, g = fp16(had(Yg) * svh_g), u likewise,
+// a = fp16(act(g, u)), A_d = fp16(had(a * suh_d) / sqrt(128)).  Y holds
+// Z / sqrt(128) from the GEMM.  A_d is written over Y_g (same positions).
+__global__ __launch_bounds__(256) void act_kernel(const int* n_sorted, const int* row_expert, int I,
+                                                  const int64_t* svh_g, const int64_t* svh_u,
+                                                  const int64_t* suh_d, int gateless, int act,
+                                                  float limit, uint16_t* y_g, const uint16_t* y_u,
+                                                  int64_t n_units) {
+    const int lane = threadIdx.x & 63;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= n_units) return;
+    const int nb = I >> 7;
+    const int row = (int)(unit / nb), j = (int)(unit % nb);
+    if (row >= *n_sorted) return;
+    const int e = row_expert[row];
+    const int c = j * 128 + 2 * lane;
+    const int64_t o = (int64_t)row * I + c;
+    float u0 = h2f(y_u, o), u1 = h2f(y_u, o + 1);
+    had128_pair(u0, u1, lane);
+    const uint16_t* svu = reinterpret_cast<const uint16_t*>(svh_u[e]);
+    u0 = (float)f32_to_f16_rne(u0 * h2f(svu, c));
+    u1 = (float)f32_to_f16_rne(u1 * h2f(svu, c + 1));
+    float g0 = 0.f, g1 = 0.f;
+    if (!gateless) {
+        g0 = h2f(y_g, o);
+        g1 = h2f(y_g, o + 1);
+        had128_pair(g0, g1, lane);
+        const uint16_t* svg = reinterpret_cast<const uint16_t*>(svh_g[e]);
+        g0 = (float)f32_to_f16_rne(g0 * h2f(svg, c));
+        g1 = (float)f32_to_f16_rne(g1 * h2f(svg, c + 1));
+    }
+    const uint16_t* sud = reinterpret_cast<const uint16_t*>(suh_d[e]);
+    float a0 = (float)f32_to_f16_rne(activate(g0, u0, act, limit)) * h2f(sud, c);
+    float a1 = (float)f32_to_f16_rne(activate(g1, u1, act, limit)) * h2f(sud, c + 1);
+    had128_pair(a0, a1, lane);
+    *reinterpret_cast<uint32_t*>(y_g + o) = pack_f16(a0 * kHadNorm, a1 * kHadNorm);
+}
+
+// out[t, block] = sum over the token's routes, in slot order, of
+// w * had(Y_d[pos]) * svh_d (Y_d = Z / sqrt(128)); sentinel routes skipped.
+// One wave per (token, 128-column block): deterministic, no atomics.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_d, int H, int T,
+                                                              int topk, const int* route_pos,
+                                                              const int* row_expert,
+                                                              const int64_t* svh_d, const void* weights,
+                                                              int w_dtype, void* out, int out_dtype) {
+    const int lane = threadIdx.x & 63;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nb = H >> 7;
+    if (unit >= (int64_t)T * nb) return;
+    const int t = (int)(unit / nb), j = (int)(unit % nb);
+    const int c = j * 128 + 2 * lane;
+    float s0 = 0.f, s1 = 0.f;
+    for (int k = 0; k < topk; ++k) {
+        const int pos = route_pos[(int64_t)t * topk + k];
+        if (pos < 0) continue;  // wave-uniform
+        float v0 = h2f(y_d, (int64_t)pos * H + c), v1 = h2f(y_d, (int64_t)pos * H + c + 1);
+        had128_pair(v0, v1, lane);
+        const uint16_t* sv = reinterpret_cast<const uint16_t*>(svh_d[row_expert[pos]]);
+        const int64_t wi = (int64_t)t * topk + k;
+        float w;
+        if (w_dtype == kF32)
+            w = reinterpret_cast<const float*>(weights)[wi];
+        else if (w_dtype == kF16)
+            w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wi]);
+        else
+            w = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wi] << 16);
+        s0 += w * (v0 * h2f(sv, c));
+        s1 += w * (v1 * h2f(sv, c + 1));
+    }
+    store_out(out, out_dtype, (int64_t)t * H + c, s0);
+    store_out(out, out_dtype, (int64_t)t * H + c + 1, s1);
+}
+
+// Drop-in output pass: rows of Z / sqrt(128) (fp32, in `src`) ->
+// had(.) * svh, written to out (scatter == 0) or added as
+// out[token_idx[r]] += route_weight[r] * value (scatter == 1).
+__global__ __launch_bounds__(256) void fat_out_kernel(const float* src, int M, int N,
+                                                      const uint16_t* svh, int scatter,
+                                                      const int64_t* token_idx,
+                                                      const uint16_t* route_weight, float* out,
+                                                      int64_t out_rows) {
+    const int lane = threadIdx.x & 63;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nb = N >> 7;
+    if (unit >= (int64_t)M * nb) return;
+    const int r = (int)(unit / nb), j = (int)(unit % nb);
+    const int c = j * 128 + 2 * lane;
+    float v0 = src[(int64_t)r * N + c], v1 = src[(int64_t)r * N + c + 1];
+    had128_pair(v0, v1, lane);
+    v0 *= h2f(svh, c);
+    v1 *= h2f(svh, c + 1);
+    if (!scatter) {
+        out[(int64_t)r * N + c] = v0;
+        out[(int64_t)r * N + c + 1] = v1;
+    } else {
+        const float w = (float)bits_to_half(route_weight[r]);
+        const int64_t d = token_idx[r];
+        if (d < 0 || d >= out_rows) return;  // wave-uniform: rows outside out are dropped
+        atomicAdd(out + d * N + c, w * v0);
+        atomicAdd(out + d * N + c + 1, w * v1);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host planning
+// ---------------------------------------------------------------------------
+inline size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+hipError_t init_fat_caps() {
+    static const hipError_t st = [] {
+        hipError_t e = hipSuccess;
+        const void* fns[] = {(const void*)fat_gemm_kernel<0>, (const void*)fat_gemm_kernel<1>,
+                             (const void*)fat_gemm_kernel<2>};
+        for (const void* f : fns) {
+            hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFatLds);
+            if (r != hipSuccess) {
+                (void)hipGetLastError();
+                e = r;
+            }
+        }
+        return e;
+    }();
+    return st;
+}
+
+void launch_fat(int cb, const FatParams& p, hipStream_t st) {
+    const int grid = ((p.n_tiles + 7) / 8) * 8;
+    switch (cb) {
+        case 0: fat_gemm_kernel<0><<<grid, kFatThreads, kFatLds, st>>>(p); break;
+        case 1: fat_gemm_kernel<1><<<grid, kFatThreads, kFatLds, st>>>(p); break;
+        default: fat_gemm_kernel<2><<<grid, kFatThreads, kFatLds, st>>>(p); break;
+    }
+}
+
+struct PrefillPlan {
+    int n_routes, max_slots, max_mtiles;
+    size_t off_route, off_agu, off_ygu, total;
+};
+
+PrefillPlan plan_prefill(int64_t T, int64_t topk, int64_t n_local, int64_t H, int64_t I, int gateless) {
+    PrefillPlan pp;
+    pp.n_routes = (int)(T * topk);
+    pp.max_slots = (int)std::min<int64_t>(pp.n_routes, n_local);
+    pp.max_mtiles = (int)route_max_mtiles(pp.n_routes, pp.max_slots, kTM);
+    const int nproj = gateless ? 1 : 2;
+    size_t off = 0;
+    pp.off_route = off;
+    off += a256(sizeof(int) * (3 + 3 * (size_t)pp.max_slots + 3 * (size_t)pp.n_routes +
+                               2 * (size_t)pp.max_mtiles));
+    pp.off_agu = off;  // A_g, A_u [n_routes][H] fp16; later Y_d [n_routes][H] fp16
+    off += a256(2 * (size_t)nproj * pp.n_routes * H);
+    pp.off_ygu = off;  // Y_g, Y_u [n_routes][I] fp16; A_d over Y_g
+    off += a256(2 * (size_t)nproj * pp.n_routes * I);
+    pp.total = off;
+    return pp;
+}
+
+}  // namespace
+}  // namespace exl3
+
+using namespace exl3;
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+static int fat_common_checks(int64_t M, int64_t tiles_k, int64_t tiles_n, int64_t K, int codebook) {
+    EXL3_CHECK(K == 2 || K == 3 || K == 4, "exl3_fat_gemm supports K in {2, 3, 4}");
+    EXL3_CHECK(codebook >= 0 && codebook <= 2, "codebook must be 0 (3INST), 1 (MCG) or 2 (mul1)");
+    EXL3_CHECK(M >= 1 && M <= (1 << 26), "exl3_fat_gemm needs 1 <= M <= 2^26 rows");
+    EXL3_CHECK(tiles_k > 0 && tiles_n > 0 && (tiles_k * 16) % 128 == 0 && (tiles_n * 16) % 128 == 0,
+               "output dimension must be divisible by 128");
+    EXL3_CHECK(tiles_k * 16 <= (1 << 20) && tiles_n * 16 <= (1 << 20), "exl3_fat_gemm dimensions too large");
+    return kOk;
+}
+
+EXL3_API int64_t exl3_fat_gemm_workspace_size(int64_t M, int64_t out_features, int scatter) {
+    if (M < 1 || out_features < 128) return 0;
+    return scatter ? (int64_t)a256(4 * (size_t)M * out_features) : 0;
+}
+
+static int fat_gemm_impl(const uint16_t* a, int64_t M, const int16_t* trellis, int64_t tiles_k,
+                         int64_t tiles_n, int64_t K, int codebook, const uint16_t* svh,
+                         const int64_t* token_idx, const uint16_t* route_weight, float* out,
+                         int64_t out_rows, void* workspace, int64_t workspace_bytes, void* stream,
+                         int scatter) {
+    const int rc = fat_common_checks(M, tiles_k, tiles_n, K, codebook);
+    if (rc) return rc;
+    EXL3_CHECK(a && trellis && svh && out && (!scatter || (token_idx && route_weight)),
+               "exl3_fat_gemm: null pointer argument");
+    const int64_t N = tiles_n * 16, K_in = tiles_k * 16;
+    const size_t need = (size_t)exl3_fat_gemm_workspace_size(M, N, scatter);
+    EXL3_CHECK(workspace_bytes >= (int64_t)need && (need == 0 || workspace),
+               "exl3_fat_gemm workspace too small: need %zu bytes", need);
+    EXL3_HIP(init_fat_caps());
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    FatParams p = {};
+    p.a = a;
+    p.lda = K_in;
+    p.trellis = reinterpret_cast<const uint8_t*>(trellis);
+    p.kuni = (int)K;
+    p.K_in = (int)K_in;
+    p.N = (int)N;
+    float* z = scatter ? reinterpret_cast<float*>(workspace) : out;
+    p.out = z;
+    p.out_f32 = 1;
+    p.ldo = N;
+    p.out_scale = kHadNorm;
+    p.grouped = 0;
+    p.M = (int)M;
+    p.n_ntiles = (int)((N + kTN - 1) / kTN);
+    const int64_t mtiles = (M + kTM - 1) / kTM;
+    EXL3_CHECK(mtiles * p.n_ntiles < (1 << 30), "exl3_fat_gemm problem too large");
+    p.n_tiles = (int)(mtiles * p.n_ntiles);
+    profile_begin_call();
+    profile_mark(0, st);
+    launch_fat(codebook, p, st);
+    EXL3_LAUNCHED();
+    profile_mark(1, st);
+    const int64_t units = M * (N / 128);
+    fat_out_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(z, (int)M, (int)N, svh, scatter,
+                                                                 token_idx, route_weight, out,
+                                                                 out_rows);
+    EXL3_LAUNCHED();
+    profile_mark(2, st);
+    return kOk;
+}
+
+EXL3_API int exl3_fat_gemm(const uint16_t* a, int64_t M, const int16_t* trellis, int64_t tiles_k,
+                           int64_t tiles_n, int64_t K, int codebook, const uint16_t* svh, float* out,
+                           void* stream) {
+    return fat_gemm_impl(a, M, trellis, tiles_k, tiles_n, K, codebook, svh, nullptr, nullptr, out,
+                         M, nullptr, 0, stream, 0);
+}
+
+EXL3_API int exl3_fat_gemm_scatter(const uint16_t* a, int64_t M, const int16_t* trellis,
+                                   int64_t tiles_k, int64_t tiles_n, int64_t K, int codebook,
+                                   const uint16_t* svh, const int64_t* token_idx,
+                                   const uint16_t* route_weight, float* out, int64_t out_rows,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+    EXL3_CHECK(out_rows >= 1, "exl3_fat_gemm_scatter needs a non-empty output");
+    return fat_gemm_impl(a, M, trellis, tiles_k, tiles_n, K, codebook, svh, token_idx, route_weight,
+                         out, out_rows, workspace, workspace_bytes, stream, 1);
+}
+
+EXL3_API int64_t exl3_moe_prefill_workspace_size(int64_t T, int64_t topk, int64_t n_local,
+                                                 int64_t hidden, int64_t inter, int gateless) {
+    if (T < 1 || topk < 1 || n_local < 1 || hidden < 128 || inter < 128) return 0;
+    return (int64_t)plan_prefill(T, topk, n_local, hidden, inter, gateless).total;
+}
+
+EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hidden, int64_t inter,
+                              const int64_t* gate_trellis, const int64_t* gate_suh,
+                              const int64_t* gate_svh, const int64_t* up_trellis,
+                              const int64_t* up_suh, const int64_t* up_svh,
+                              const int64_t* down_trellis, const int64_t* down_suh,
+                              const int64_t* down_svh, int64_t n_local, const int8_t* k_gate,
+                              const int8_t* k_up, const int8_t* k_down, int64_t K_gate,
+                              int64_t K_up, int64_t K_down, int codebook, int gateless, int act,
+                              float swiglu_limit, const void* ids, int ids_dtype,
+                              const void* weights, int w_dtype, int64_t topk,
+                              const int32_t* n_valid, void* out, int out_dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+    EXL3_CHECK(n_local >= 1 && n_local <= kRouteMaxLocal,
+               "fused MoE prefill supports 1 <= n_local <= %d local experts", kRouteMaxLocal);
+    EXL3_CHECK(T >= 1 && topk >= 1 && T * topk <= (1 << 22),
+               "fused MoE prefill supports 1 <= T*topk <= 2^22 routes");
+    EXL3_CHECK(hidden > 0 && hidden % 128 == 0,
+               "fused MoE hidden width must be a positive multiple of 128");
+    EXL3_CHECK(inter > 0 && inter % 128 == 0,
+               "fused MoE local intermediate width must be a positive multiple of 128");
+    EXL3_CHECK(hidden <= (1 << 20) && inter <= (1 << 20), "fused MoE dimensions too large");
+    EXL3_CHECK(std::isfinite(swiglu_limit) && swiglu_limit >= 0.0f,
+               "fused MoE SwiGLU limit must be finite and nonnegative (0 disables clipping)");
+    EXL3_CHECK(codebook >= 0 && codebook <= 2, "codebook must be 0 (3INST), 1 (MCG) or 2 (mul1)");
+    EXL3_CHECK(act == kActSilu || act == kActRelu2 || act == kActSwigluOai,
+               "fused MoE activation must be 0 (silu), 2 (relu2, gateless) or 3 (swiglu-oai)");
+    EXL3_CHECK(!gateless || act == kActRelu2, "a gateless layer uses the relu2 activation");
+    EXL3_CHECK(x_dtype >= 0 && x_dtype <= 2 && w_dtype >= 0 && w_dtype <= 2 && out_dtype >= 0 &&
+                   out_dtype <= 2 && (ids_dtype == 0 || ids_dtype == 1),
+               "dtype ids: values 0 fp16, 1 bf16, 2 fp32; ids 0 int32, 1 int64");
+    const int64_t Ks[3] = {K_gate, K_up, K_down};
+    const int8_t* kt[3] = {k_gate, k_up, k_down};
+    for (int i = 0; i < 3; ++i)
+        EXL3_CHECK(kt[i] || (Ks[i] >= 2 && Ks[i] <= 4),
+                   "fused MoE K must be 2, 3 or 4 (or come from a per-expert K table)");
+    EXL3_CHECK(x && ids && weights && out && up_trellis && up_suh && up_svh && down_trellis &&
+                   down_suh && down_svh && (gateless || (gate_trellis && gate_suh && gate_svh)),
+               "fused MoE: null pointer argument");
+    const PrefillPlan pp = plan_prefill(T, topk, n_local, hidden, inter, gateless);
+    EXL3_CHECK(workspace && workspace_bytes >= (int64_t)pp.total,
+               "fused MoE prefill workspace too small: need %zu bytes", pp.total);
+    EXL3_HIP(init_fat_caps());
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    const int nproj = gateless ? 1 : 2;
+
+    profile_begin_call();
+    profile_mark(0, st);
+    RouteOut ro = {};
+    int* rb = reinterpret_cast<int*>(ws + pp.off_route);
+    ro.n_active = rb;
+    ro.n_mtiles = rb + 1;
+    int* n_sorted = rb + 2;
+    ro.slot_expert = rb + 3;
+    ro.slot_start = ro.slot_expert + pp.max_slots;
+    ro.slot_rows = ro.slot_start + pp.max_slots;
+    ro.row_token = ro.slot_rows + pp.max_slots;
+    ro.row_expert = ro.row_token + pp.n_routes;
+    ro.route_pos = ro.row_expert + pp.n_routes;
+    ro.mt_slot = ro.route_pos + pp.n_routes;
+    ro.mt_row0 = ro.mt_slot + pp.max_mtiles;
+    ro.n_sorted = n_sorted;
+    EXL3_HIP(launch_route(ids, ids_dtype, pp.n_routes, (int)topk, (int)n_local, n_valid, kTM, ro, st));
+
+    uint16_t* a_g = reinterpret_cast<uint16_t*>(ws + pp.off_agu);
+    uint16_t* a_u = a_g + (size_t)(nproj - 1) * pp.n_routes * hidden;
+    uint16_t* y_g = reinterpret_cast<uint16_t*>(ws + pp.off_ygu);
+    uint16_t* y_u = y_g + (size_t)(nproj - 1) * pp.n_routes * inter;
+    const int64_t* gtab_t = gateless ? up_trellis : gate_trellis;
+    const int64_t* gtab_su = gateless ? up_suh : gate_suh;
+    const int64_t* gtab_sv = gateless ? up_svh : gate_svh;
+
+    profile_mark(1, st);
+    {
+        const int64_t units = (int64_t)pp.n_routes * (hidden / 128);
+        rotate_in_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
+            x, x_dtype, hidden, (int)hidden, n_sorted, ro.row_token, ro.row_expert,
+            gateless ? up_suh : gate_suh, up_suh, nproj, gateless ? a_u : a_g, a_u, units);
+        EXL3_LAUNCHED();
+    }
+    profile_mark(2, st);
+    FatParams p = {};
+    p.lda = hidden;
+    p.K_in = (int)hidden;
+    p.N = (int)inter;
+    p.out_f32 = 0;
+    p.ldo = inter;
+    p.out_scale = kHadNorm;
+    p.grouped = 1;
+    p.n_mtiles = ro.n_mtiles;
+    p.mt_slot = ro.mt_slot;
+    p.mt_row0 = ro.mt_row0;
+    p.slot_expert = ro.slot_expert;
+    p.slot_start = ro.slot_start;
+    p.slot_rows = ro.slot_rows;
+    p.n_ntiles = (int)((inter + kTN - 1) / kTN);
+    p.n_tiles = pp.max_mtiles * p.n_ntiles;
+    for (int q = 0; q < nproj; ++q) {
+        const bool up = gateless || q == 1;
+        p.a = up ? a_u : a_g;
+        p.trellis_tab = up ? up_trellis : gtab_t;
+        p.ktab = up ? k_up : k_gate;
+        p.kuni = (int)(up ? K_up : K_gate);
+        p.out = up ? y_u : y_g;
+        launch_fat(codebook, p, st);
+        EXL3_LAUNCHED();
+    }
+    (void)gtab_su;
+    profile_mark(3, st);
+    {
+        const int64_t units = (int64_t)pp.n_routes * (inter / 128);
+        act_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
+            n_sorted, ro.row_expert, (int)inter, gtab_sv, up_svh, down_suh, gateless, act,
+            swiglu_limit, gateless ? y_u : y_g, y_u, units);
+        EXL3_LAUNCHED();
+    }
+    profile_mark(4, st);
+    uint16_t* y_d = a_g;  // A_g/A_u are dead: Y_d [n_routes][hidden] fp16
+    p.a = gateless ? y_u : y_g;
+    p.lda = inter;
+    p.K_in = (int)inter;
+    p.N = (int)hidden;
+    p.trellis_tab = down_trellis;
+    p.ktab = k_down;
+    p.kuni = (int)K_down;
+    p.out = y_d;
+    p.ldo = hidden;
+    p.n_ntiles = (int)((hidden + kTN - 1) / kTN);
+    p.n_tiles = pp.max_mtiles * p.n_ntiles;
+    launch_fat(codebook, p, st);
+    EXL3_LAUNCHED();
+    profile_mark(5, st);
+    {
+        const int64_t units = T * (hidden / 128);
+        prefill_combine_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
+            y_d, (int)hidden, (int)T, (int)topk, ro.route_pos, ro.row_expert, down_svh, weights,
+            w_dtype, out, out_dtype);
+        EXL3_LAUNCHED();
+    }
+    profile_mark(6, st);
+    return kOk;
+}

@@ -17,6 +17,7 @@
 //                (csrc/p2b_moe.cu:1976-2008): deterministic, no atomics.
 #include "gemv_core.h"
 #include "profile.h"
+#include "route.h"
 
 #include <cmath>
 
@@ -25,9 +26,9 @@ namespace {
 
 constexpr int kMaxMRB = 16;       // activation rows per row group (one MFMA row block)
 constexpr int kMoeMRB = 8;        // row-group size of the MoE phases
-constexpr int kMaxRoutes = 8192;  // routes sortable by the single-workgroup router
+constexpr int kMaxRoutes = 8192;  // routes sortable by the bitonic router
+constexpr int64_t kMaxRoutesMultisplit = 1 << 20;  // routes of the multisplit router
 constexpr int kRouteBits = 13;    // log2(kMaxRoutes)
-constexpr int kRouteThreads = 1024;
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
@@ -438,22 +439,17 @@ __global__ __launch_bounds__(256) void linear_finish_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Routing: stable sort of the T*topk routes by local expert id (sentinel
-// routes last), then slots = runs of one expert.  One workgroup.
+// Routing for layers with more than kRouteMaxLocal local experts: bitonic
+// sort of the T*topk routes by local expert id (sentinel routes last) in one
+// workgroup, then slots = runs of one expert.  Same outputs as the multisplit
+// router of route.hip (which handles every layer up to kRouteMaxLocal
+// experts); at most kMaxRoutes routes.
 // ---------------------------------------------------------------------------
-struct RouteOut {
-    int* n_active;    // [1]
-    int* slot_expert; // [max_slots]
-    int* slot_start;  // [max_slots]
-    int* slot_rows;   // [max_slots]
-    int* row_token;   // [n_routes]: sorted row -> token
-    int* row_expert;  // [n_routes]: sorted row -> local expert
-    int* route_pos;   // [n_routes]: route (t*topk+k) -> sorted row, or -1
-};
-
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(const void* ids, int ids_i64, int n_routes,
-                                                              int topk, int n_local,
-                                                              const int32_t* n_valid, RouteOut o) {
+__global__ __launch_bounds__(kRouteThreads) void route_bitonic_kernel(const void* ids, int ids_i64,
+                                                                     int n_routes, int topk,
+                                                                     int n_local,
+                                                                     const int32_t* n_valid,
+                                                                     RouteOut o) {
     __shared__ uint32_t key[kMaxRoutes];
     __shared__ int wave_sum[kRouteThreads / 64];
     const int tid = threadIdx.x;
@@ -792,15 +788,17 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
                               const void* weights, int w_dtype, int64_t topk,
                               const int32_t* n_valid, void* out, int out_dtype, void* workspace,
                               int64_t workspace_bytes, void* stream) {
-    EXL3_CHECK(T >= 1 && topk >= 1 && T * topk <= kMaxRoutes,
-               "fused MoE decode supports 1 <= T*topk <= %d routes", kMaxRoutes);
+    EXL3_CHECK(n_local >= 1 && n_local < (1 << 18), "fused MoE n_local must be in [1, 2^18)");
+    const int64_t max_routes = n_local <= kRouteMaxLocal ? kMaxRoutesMultisplit : kMaxRoutes;
+    EXL3_CHECK(T >= 1 && topk >= 1 && T * topk <= max_routes,
+               "fused MoE decode supports 1 <= T*topk <= %lld routes with %lld local experts",
+               (long long)max_routes, (long long)n_local);
     EXL3_CHECK(topk <= kMaxTopk, "fused MoE supports topk <= %d", kMaxTopk);
     EXL3_CHECK(hidden > 0 && hidden % 128 == 0,
                "fused MoE hidden width must be a positive multiple of 128");
     EXL3_CHECK(inter > 0 && inter % 128 == 0,
                "fused MoE local intermediate width must be a positive multiple of 128");
     EXL3_CHECK(hidden <= (1 << 20) && inter <= (1 << 20), "fused MoE dimensions too large");
-    EXL3_CHECK(n_local >= 1 && n_local < (1 << 18), "fused MoE n_local must be in [1, 2^18)");
     EXL3_CHECK(std::isfinite(swiglu_limit) && swiglu_limit >= 0.0f,
                "fused MoE SwiGLU limit must be finite and nonnegative (0 disables clipping)");
     EXL3_CHECK(codebook >= 0 && codebook <= 2, "codebook must be 0 (3INST), 1 (MCG) or 2 (mul1)");
@@ -827,7 +825,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
 
     profile_begin_call();
     profile_mark(0, st);
-    RouteOut ro;
+    RouteOut ro = {};
     int* rbase = reinterpret_cast<int*>(ws + mp.off_route);
     ro.n_active = rbase;
     ro.slot_expert = rbase + 1;
@@ -836,9 +834,14 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     ro.row_token = ro.slot_rows + mp.max_slots;
     ro.row_expert = ro.row_token + mp.n_routes;
     ro.route_pos = ro.row_expert + mp.n_routes;
-    route_kernel<<<1, kRouteThreads, 0, st>>>(ids, ids_dtype, mp.n_routes, (int)topk, (int)n_local,
-                                              n_valid, ro);
-    EXL3_LAUNCHED();
+    if (n_local <= kRouteMaxLocal) {
+        EXL3_HIP(launch_route(ids, ids_dtype, mp.n_routes, (int)topk, (int)n_local, n_valid, 0, ro,
+                              st));
+    } else {
+        route_bitonic_kernel<<<1, kRouteThreads, 0, st>>>(ids, ids_dtype, mp.n_routes, (int)topk,
+                                                          (int)n_local, n_valid, ro);
+        EXL3_LAUNCHED();
+    }
 
     GemvParams p = {};
     const int64_t* tabs[9] = {gateless ? up_trellis : gate_trellis, gateless ? up_suh : gate_suh,

@@ -205,17 +205,11 @@ def exl3_gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: to
 ACT_SILU, ACT_RELU2, ACT_SWIGLU_OAI = 0, 2, 3
 
 
-def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
-                tables: dict[str, torch.Tensor], n_local: int, intermediate_size: int, *,
-                K: tuple[int, int, int] = (4, 4, 4), k_tables: tuple | None = None,
-                codebook: int = CB_MCG, gateless: bool = False, act: int = ACT_SILU,
-                swiglu_limit: float = 0.0, n_valid: torch.Tensor | None = None,
-                out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """All T rows of a routed-expert layer in one launch sequence.
-
-    ``tables`` holds the nine int64 pointer tables (keys gate_trellis, gate_suh,
-    gate_svh, up_*, down_*), one entry per local expert.  ``ids`` [T, topk]
-    local ids; ids outside [0, n_local) are skipped.  Returns [T, hidden]."""
+def _moe_call(entry: str, ws_query: str, ws_kind: str, x: torch.Tensor, ids: torch.Tensor,
+              weights: torch.Tensor, tables: dict[str, torch.Tensor], n_local: int,
+              intermediate_size: int, K, k_tables, codebook: int, gateless: bool, act: int,
+              swiglu_limit: float, n_valid: torch.Tensor | None, out: torch.Tensor | None,
+              out_dtype: torch.dtype) -> torch.Tensor:
     _check(x.dim() == 2 and x.is_cuda, "fused MoE requires a CUDA [T, hidden] input")
     T, hidden = x.shape
     _check(ids.dim() == 2 and ids.size(0) == T, "fused MoE ids must be [T, topk]")
@@ -257,11 +251,11 @@ def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
     _check(out.shape == (T, hidden) and out.is_contiguous() and out.device == dev,
            "fused MoE output shape must match input")
     lib = _lib.load()
-    need = int(lib.exl3_moe_workspace_size(T, topk, n_local, hidden, intermediate_size, int(gateless)))
+    need = int(getattr(lib, ws_query)(T, topk, n_local, hidden, intermediate_size, int(gateless)))
     _check(need > 0, "fused MoE: unsupported geometry")
-    ws = workspace(dev, "moe", need)
+    ws = workspace(dev, ws_kind, need)
     with torch.cuda.device(dev):
-        _lib.call("exl3_moe_forward", xs.data_ptr(), _dtype_id(xs, "x"), T, hidden,
+        _lib.call(entry, xs.data_ptr(), _dtype_id(xs, "x"), T, hidden,
                   int(intermediate_size), *ptrs, int(n_local), kt[0], kt[1], kt[2],
                   int(K[0]), int(K[1]), int(K[2]), int(codebook), int(gateless), int(act),
                   float(swiglu_limit), ids_c.data_ptr(), 1 if ids_c.dtype == torch.int64 else 0,
@@ -269,6 +263,109 @@ def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                   n_valid.data_ptr() if n_valid is not None else None, out.data_ptr(),
                   _dtype_id(out, "out"), ws.data_ptr(), ws.numel(), stream_of(dev))
     return out
+
+
+def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+                tables: dict[str, torch.Tensor], n_local: int, intermediate_size: int, *,
+                K: tuple[int, int, int] = (4, 4, 4), k_tables: tuple | None = None,
+                codebook: int = CB_MCG, gateless: bool = False, act: int = ACT_SILU,
+                swiglu_limit: float = 0.0, n_valid: torch.Tensor | None = None,
+                out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """All T decode rows of a routed-expert layer in one launch sequence
+    (streaming GEMV executor; weights are streamed once per 8 rows of a slot).
+
+    ``tables`` holds the nine int64 pointer tables (keys gate_trellis, gate_suh,
+    gate_svh, up_*, down_*), one entry per local expert.  ``ids`` [T, topk]
+    local ids; ids outside [0, n_local) are skipped.  Returns [T, hidden]."""
+    return _moe_call("exl3_moe_forward", "exl3_moe_workspace_size", "moe", x, ids, weights, tables,
+                     n_local, intermediate_size, K, k_tables, codebook, gateless, act, swiglu_limit,
+                     n_valid, out, out_dtype)
+
+
+def moe_prefill(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+                tables: dict[str, torch.Tensor], n_local: int, intermediate_size: int, *,
+                K: tuple[int, int, int] = (4, 4, 4), k_tables: tuple | None = None,
+                codebook: int = CB_MCG, gateless: bool = False, act: int = ACT_SILU,
+                swiglu_limit: float = 0.0, n_valid: torch.Tensor | None = None,
+                out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Same contract as :func:`moe_forward` on the prefill executor (grouped
+    MFMA fat GEMMs: each routed expert's packed weights are decoded once per
+    256 routed rows).  The reference reaches this regime through
+    apply_exl3_fused_moe / apply_exl3_batched_fat (src/vllm_exl3/exl3.py:
+    2981-3599); n_local <= 1023."""
+    return _moe_call("exl3_moe_prefill", "exl3_moe_prefill_workspace_size", "moe_prefill", x, ids,
+                     weights, tables, n_local, intermediate_size, K, k_tables, codebook, gateless,
+                     act, swiglu_limit, n_valid, out, out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# Prefill fat GEMM (csrc/bindings.cpp:259-265)
+# ---------------------------------------------------------------------------
+
+def _check_fat(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor,
+               K: int) -> None:
+    _check(a.is_cuda and packed.is_cuda and out.is_cuda and svh.is_cuda,
+           "exl3_fat_gemm tensors must be CUDA tensors")
+    _check(a.is_contiguous() and packed.is_contiguous() and out.is_contiguous()
+           and svh.is_contiguous(), "exl3_fat_gemm tensors must be contiguous")
+    _check(a.dtype == torch.float16, "a must be float16")
+    _check(packed.dtype == torch.int16, "packed must be int16")
+    _check(out.dtype == torch.float32, "out must be float32")
+    _check(svh.dtype == torch.float16, "svh must be float16")
+    _check(a.dim() == 2 and packed.dim() == 3 and out.dim() == 2 and svh.dim() == 1,
+           "exl3_fat_gemm expects rank-2/rank-3 tensors")
+    _check(K in (2, 3, 4), "exl3_fat_gemm supports K in {2, 3, 4}")
+    _check(a.size(1) == packed.size(0) * 16, "a K dimension does not match packed tensor")
+    _check(svh.numel() == packed.size(1) * 16, "svh N dimension does not match packed tensor")
+    _check(svh.numel() % 128 == 0 and a.size(1) % 128 == 0,
+           "output dimension must be divisible by 128")
+    _check(packed.size(2) == 16 * K, "packed block width must be 16*K int16 words")
+    _check(a.device == packed.device == out.device == svh.device,
+           "exl3_fat_gemm tensors must share a device")
+
+
+def exl3_fat_gemm(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor,
+                  K: int, mcg: bool, mul1: bool, *, codebook: int | None = None) -> None:
+    """out[M, N] = had128(a @ Wq) * svh in fp32 (a already input-rotated).
+    csrc/bindings.cpp:259-261 / csrc/exl3_fat_gemm.cu:277-287; any K in
+    {2,3,4} and codebook here."""
+    K = int(K)
+    _check_fat(a, packed, out, svh, K)
+    _check(out.size(0) == a.size(0) and out.size(1) == svh.numel(), "out shape must be [M, N]")
+    cb = codebook_id(mcg, mul1, codebook)
+    dev = a.device
+    with torch.cuda.device(dev):
+        _lib.call("exl3_fat_gemm", a.data_ptr(), a.size(0), packed.data_ptr(), packed.size(0),
+                  packed.size(1), K, cb, svh.data_ptr(), out.data_ptr(), stream_of(dev))
+
+
+def exl3_fat_gemm_scatter(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor,
+                          svh: torch.Tensor, token_idx: torch.Tensor, route_weight: torch.Tensor,
+                          K: int, mcg: bool, mul1: bool, *, codebook: int | None = None) -> None:
+    """out[token_idx[r]] += route_weight[r] * (had128(a @ Wq) * svh)[r].
+    csrc/bindings.cpp:262-265 / csrc/exl3_fat_gemm.cu:289-305."""
+    K = int(K)
+    _check_fat(a, packed, out, svh, K)
+    _check(out.size(1) == svh.numel(), "out N dimension mismatch")
+    _check(token_idx.is_cuda and route_weight.is_cuda, "routing tensors must be CUDA tensors")
+    _check(token_idx.is_contiguous() and route_weight.is_contiguous(),
+           "routing tensors must be contiguous")
+    _check(token_idx.dtype == torch.int64, "token_idx must be int64")
+    _check(route_weight.dtype == torch.float16, "route_weight must be float16")
+    _check(token_idx.numel() == a.size(0) and route_weight.numel() == a.size(0),
+           "routing tensors must have M elements")
+    _check(token_idx.device == a.device and route_weight.device == a.device,
+           "routing tensors must share a device with a")
+    cb = codebook_id(mcg, mul1, codebook)
+    dev = a.device
+    lib = _lib.load()
+    need = int(lib.exl3_fat_gemm_workspace_size(a.size(0), svh.numel(), 1))
+    ws = workspace(dev, "fat_scatter", need)
+    with torch.cuda.device(dev):
+        _lib.call("exl3_fat_gemm_scatter", a.data_ptr(), a.size(0), packed.data_ptr(),
+                  packed.size(0), packed.size(1), K, cb, svh.data_ptr(), token_idx.data_ptr(),
+                  route_weight.data_ptr(), out.data_ptr(), out.size(0), ws.data_ptr(), ws.numel(),
+                  stream_of(dev))
 
 
 def _check_fused_common(prefix: str, x, out, ptr_tables, intermediate_size, swiglu_limit) -> None:
