@@ -26,6 +26,8 @@ import platform
 import sys
 import time
 
+import numpy as np
+
 ROOT = pathlib.Path(__file__).resolve().parent
 for p in (ROOT / "vllm-exl3_amd", ROOT / "oracle"):
     sys.path.insert(0, str(p))
@@ -128,6 +130,119 @@ def cpu_baseline(S, O, torch, experts, ids_np, x, budget_s=12.0):
     }
 
 
+# ---------------------------------------------------------------------------
+# Other BASELINE configurations, reported beside the headline
+# ---------------------------------------------------------------------------
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def time_steps(torch, fn, steps, warmup, PhaseTimer=None):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    pt = None
+    if PhaseTimer is not None:
+        pt = PhaseTimer(max_calls=steps)
+        pt.__enter__()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    if pt is not None:
+        pt.__exit__(None, None, None)
+    return start.elapsed_time(end) / steps, pt
+
+
+def prefill_c2(C, S, torch, dev, steps, warmup, PhaseTimer):
+    """Config 2: routed-MoE prefill, E128 top-8, H4096, I1024, K4 MCG,
+    T=2048 tokens with Zipf(1.1) expert popularity."""
+    E2, H2, I2, T2, K2 = 128, 4096, 1024, 2048, 4
+    layer2 = S.moe_layer_device(2, E2, H2, I2, K2, dev)
+    ids_np, w_np = S.zipf_topk(2, T2, E2, TOPK)
+    x = torch.from_numpy(S.activations(2, T2, H2)).to(dev).bfloat16()
+    ids = torch.from_numpy(ids_np).to(dev)
+    w = torch.from_numpy(w_np).to(dev)
+    out = torch.empty((T2, H2), dtype=torch.float32, device=dev)
+
+    def step():
+        C.moe_prefill(x, ids, w, layer2, E2, I2, K=(K2, K2, K2), codebook=1, out=out)
+
+    ms, pt = time_steps(torch, step, steps, warmup, PhaseTimer)
+    routes = T2 * TOPK
+    flops = 2.0 * routes * (2 * H2 * I2 + I2 * H2)
+    gu_flops = 2.0 * routes * 2 * H2 * I2
+    names = ("route", "rotate_in", "gate_up_gemm", "act", "down_gemm", "combine")
+    phase = {n: pt.mean_ms(i) * 1e3 for i, n in enumerate(names)}
+    gemm_us = phase["gate_up_gemm"] + phase["down_gemm"]
+    rows = np.bincount(ids_np.ravel(), minlength=E2)
+    del layer2
+    return {
+        "workload": f"C2 routed-MoE prefill, E{E2} top-{TOPK}, H{H2} I{I2}, K{K2} MCG, T={T2}, Zipf(1.1)",
+        "us_per_step": round(ms * 1e3, 2),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "frac_fp16_peak": round(flops / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+        "gemm_tflops": round(flops / (gemm_us * 1e-6) / 1e12, 2),
+        "gate_up_gemm_tflops": round(gu_flops / (phase["gate_up_gemm"] * 1e-6) / 1e12, 2),
+        "flops_per_step": flops,
+        "rows_per_expert": {"min": int(rows.min()), "max": int(rows.max())},
+        "phase_us": {k: round(v, 2) for k, v in phase.items()},
+    }
+
+
+def decode_c3(C, S, torch, dev, steps, warmup, PhaseTimer):
+    """Config 3: mixed-K routed-MoE decode, 256 routed experts (40/40/20
+    K2/K3/K4, MCG) + 1 shared K4 expert (routed as a ninth slot of weight 1),
+    top-8, H6144, I2048, T=64 uniform softmax routing."""
+    E3, H3, I3, T3 = 256, 6144, 2048, 64
+    ks = S.mixed_k(3, E3) + [4]
+    layer3 = S.moe_layer_device(3, E3 + 1, H3, I3, ks, dev)
+    ids_np, w_np = S.softmax_topk(3, T3, E3, TOPK)
+    ids_np = np.concatenate([ids_np, np.full((T3, 1), E3, np.int64)], axis=1)
+    w_np = np.concatenate([w_np, np.ones((T3, 1), np.float32)], axis=1)
+    x = torch.from_numpy(S.activations(3, T3, H3)).to(dev).bfloat16()
+    ids = torch.from_numpy(ids_np).to(dev)
+    w = torch.from_numpy(w_np).to(dev)
+    out = torch.empty((T3, H3), dtype=torch.float32, device=dev)
+
+    def step():
+        C.moe_forward(x, ids, w, layer3, E3 + 1, I3, K=(4, 4, 4), k_tables=layer3["k_tables"],
+                      codebook=1, out=out)
+
+    ms, pt = time_steps(torch, step, steps, warmup, PhaseTimer)
+    used = sorted(set(ids_np.ravel().tolist()))
+    nbytes = sum(ks[e] * 3 * H3 * I3 // 8 + 6 * (H3 + I3) for e in used) + 2 * T3 * H3 + 4 * T3 * H3
+    del layer3
+    return {
+        "workload": f"C3 mixed-K MoE decode, E{E3}+1 shared, top-{TOPK}, H{H3} I{I3}, "
+                    f"K2/K3/K4 40/40/20 MCG, T={T3}",
+        "us_per_step": round(ms * 1e3, 2),
+        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_step": nbytes,
+        "distinct_experts": len(used),
+        "phase_us": {n: round(pt.mean_ms(i) * 1e3, 2)
+                     for i, n in enumerate(("route", "gate_up", "down", "combine"))},
+    }
+
+
+def linear_c0(C, S, torch, dev, steps, warmup):
+    """Config 0 on the GPU: one EXL3 linear 2048x2048, K4 MCG, batch 1 and 16."""
+    lin = S.linear(0, 2048, 2048, 4)
+    t = torch.from_numpy(lin["trellis"]).to(dev)
+    su = torch.from_numpy(lin["suh"]).to(dev)
+    sv = torch.from_numpy(lin["svh"]).to(dev)
+    res = {}
+    for m in (1, 16):
+        x = torch.from_numpy(S.activations(100 + m, m, 2048)).to(dev).half()
+        ms, _ = time_steps(torch, lambda: C.exl3_gemm(x, t, su, sv, 4, True), steps, warmup)
+        nbytes = 2048 * 2048 * 4 // 8 + 2 * 4096 + 2 * m * 4096
+        res[f"m={m}"] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    return {"workload": "C0 EXL3 linear 2048x2048, K4 MCG, fp16 x", **res}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -136,6 +251,8 @@ def main() -> int:
     ap.add_argument("--batches", default="1,4,16",
                     help="decode batch sizes T to run; the headline is the largest")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--configs", default="c0,c2,c3",
+                    help="other BASELINE configs reported beside the headline (c0,c2,c3; '' = none)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
@@ -206,6 +323,14 @@ def main() -> int:
             for T, r in results.items()
         },
     }
+    others = {c.strip() for c in args.configs.split(",") if c.strip()}
+    if "c0" in others:
+        line["linear_c0"] = linear_c0(C, S, torch, dev, args.steps, args.warmup)
+    if "c2" in others:
+        line["prefill_c2"] = prefill_c2(C, S, torch, dev, max(5, args.steps // 5),
+                                        min(args.warmup, 3), PhaseTimer)
+    if "c3" in others:
+        line["mixed_k_c3"] = decode_c3(C, S, torch, dev, args.steps, args.warmup, PhaseTimer)
     if not args.no_cpu_baseline:
         import oracle as O
 

@@ -104,6 +104,51 @@ def zipf_topk(seed: int, tokens: int, n_experts: int, topk: int, s: float = 1.1)
     return ids, w
 
 
+def moe_layer_device(seed: int, n_experts: int, hidden: int, inter: int, K, device) -> dict:
+    """Like ``to_device(moe_layer(...))`` but generated on the device with
+    torch's seeded generator (for multi-GB layers; the bits differ from the
+    numpy generator's, the distributions are the same).  ``K`` is an int or a
+    per-expert sequence of ints."""
+    import torch
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+
+    def bits(in_f, out_f, k):
+        t = torch.randint(-(1 << 15), 1 << 15, (in_f // 16, out_f // 16, 16 * k),
+                          dtype=torch.int32, device=device, generator=gen)
+        return t.to(torch.int16)
+
+    def signs(n):
+        return torch.where(torch.rand(n, device=device, generator=gen) < 0.5, -1.0, 1.0)
+
+    def su(n):
+        return signs(n).half()
+
+    def sv(n):
+        u = 0.005 + 0.015 * torch.rand(n, device=device, generator=gen)
+        return (signs(n) * u).half()
+
+    store = []
+    names = ("gate", "up", "down")
+    tabs = {f"{p}_{a}": [] for p in names for a in ("trellis", "suh", "svh")}
+    ks = {p: [] for p in names}
+    for e in range(n_experts):
+        k = int(K if isinstance(K, (int, np.integer)) else K[e])
+        for p in names:
+            i_f, o_f = (hidden, inter) if p != "down" else (inter, hidden)
+            t, s_u, s_v = bits(i_f, o_f, k), su(i_f), sv(o_f)
+            store += [t, s_u, s_v]
+            tabs[f"{p}_trellis"].append(t.data_ptr())
+            tabs[f"{p}_suh"].append(s_u.data_ptr())
+            tabs[f"{p}_svh"].append(s_v.data_ptr())
+            ks[p].append(k)
+    out = {k: torch.tensor(v, dtype=torch.int64, device=device) for k, v in tabs.items()}
+    out["k_tables"] = tuple(torch.tensor(ks[p], dtype=torch.int8, device=device) for p in names)
+    out["_store"] = store
+    return out
+
+
 def to_device(experts: list, device) -> dict:
     """Upload packs and build the nine int64 pointer tables plus int8 K tables.
 
