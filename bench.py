@@ -243,6 +243,41 @@ def linear_c0(C, S, torch, dev, steps, warmup):
     return {"workload": "C0 EXL3 linear 2048x2048, K4 MCG, fp16 x", **res}
 
 
+def kv_decode_c4(S, torch, dev, steps, warmup, PhaseTimer):
+    """Config 4: int4 paged KV-cache decode attention, B16, Hq64, Hkv8, d128,
+    32768 cached tokens per sequence in 16-token pages, random block table."""
+    from vllm_exl3_amd import kv_int4 as KV
+
+    B4, Hq4, Hkv4, L4 = 16, 64, 8, 32768
+    max_pages = L4 // 16
+    k, v = S.kv_inputs_device(4, B4, Hkv4, L4, dev)
+    bt = torch.from_numpy(S.block_table(4, B4, max_pages)).to(dev)
+    st = torch.full((B4,), L4, dtype=torch.int32, device=dev)
+    pool = KV.new_pool(B4 * max_pages, Hkv4, dev)
+    KV.pack_pages(k, v, st, bt, pool)
+    del k, v
+    q = torch.from_numpy(S.activations(4, B4 * Hq4, 128).reshape(B4, Hq4, 128)).to(dev).bfloat16()
+    out = torch.empty_like(q)
+    scale = 1.0 / 128 ** 0.5
+    ms, pt = time_steps(torch, lambda: KV.int4_decode(q, pool, bt, st, Hkv4, scale, out),
+                        steps, warmup, PhaseTimer)
+    cache_bytes = B4 * Hkv4 * L4 * 160
+    nbytes = cache_bytes + 2 * q.numel() * 2 + bt.numel() * 4
+    att_us = pt.mean_ms(0) * 1e3
+    del pool
+    return {
+        "workload": f"C4 int4 paged KV decode attention, B{B4} Hq{Hq4} Hkv{Hkv4} d128, "
+                    f"L={L4}, 16-token pages",
+        "us_per_step": round(ms * 1e3, 2),
+        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_step": nbytes,
+        "attention_kernel_us": round(att_us, 2),
+        "attention_kernel_gbs": round(cache_bytes / (att_us * 1e-6) / 1e9, 1),
+        "merge_us": round(pt.mean_ms(1) * 1e3, 2),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,8 +286,8 @@ def main() -> int:
     ap.add_argument("--batches", default="1,4,16",
                     help="decode batch sizes T to run; the headline is the largest")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--configs", default="c0,c2,c3",
-                    help="other BASELINE configs reported beside the headline (c0,c2,c3; '' = none)")
+    ap.add_argument("--configs", default="c0,c2,c3,c4",
+                    help="other BASELINE configs reported beside the headline (c0,c2,c3,c4; '' = none)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
@@ -331,6 +366,8 @@ def main() -> int:
                                         min(args.warmup, 3), PhaseTimer)
     if "c3" in others:
         line["mixed_k_c3"] = decode_c3(C, S, torch, dev, args.steps, args.warmup, PhaseTimer)
+    if "c4" in others:
+        line["kv_decode_c4"] = kv_decode_c4(S, torch, dev, args.steps, args.warmup, PhaseTimer)
     if not args.no_cpu_baseline:
         import oracle as O
 

@@ -155,6 +155,56 @@ int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hidden, int6
                      void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Paged int4 KV cache (format defined by this build; the reference's own
+ * 4-bit KV cache is NVFP4).  Per (token, KV head, 32-dim group) an fp16
+ * scale and zero, codes 0..15; pages of 16 tokens; one page of one KV head
+ * is exl3_kv_page_bytes() = 2560 bytes (K codes, V codes, K scale, K zero,
+ * V scale, V zero).  The pool is uint8 [num_pages, num_kv_heads, 2560];
+ * block_table is int32 [B, >= max_pages] (row stride bt_stride elements),
+ * seq_lens int32 [B].  head_dim is 128.
+ * ------------------------------------------------------------------------- */
+int64_t exl3_kv_page_bytes(void);
+
+/* Quantise K and V [B, num_kv_heads, L, 128] (element strides stride_b,
+ * stride_h, stride_t; dtype 0 fp16, 1 bf16, 2 fp32) into the pages the block
+ * table assigns to tokens [0, seq_lens[b]).  Token slots of a last page past
+ * seq_lens[b] get code 0, scale 0, zero 0.
+ * Replaces the cache write side of the reference's 4-bit KV overlay
+ * (pack_q4_row / _q4_w1_kernel, src/vllm_exl3/minimax_q4kv_reference.py:
+ * 297-326, src/vllm_exl3/minimax_q4kv_kernels.py:216-348). */
+int exl3_kv_pack_pages(const void* k, const void* v, int kv_dtype, int64_t B, int64_t num_kv_heads,
+                       int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                       const int32_t* seq_lens, const int32_t* block_table, int64_t bt_stride,
+                       int64_t max_pages, uint8_t* pool, int64_t num_pages, void* stream);
+
+/* Dequantise the cached tokens back to fp32 K, V [B, num_kv_heads, L, 128]
+ * (code * scale + zero); positions past seq_lens[b] are not written.
+ * Replaces dequant_pool_pages (src/vllm_exl3/minimax_q4kv_reference.py:735-776). */
+int exl3_kv_unpack_pages(const uint8_t* pool, int64_t num_pages, int64_t num_kv_heads,
+                         const int32_t* seq_lens, const int32_t* block_table, int64_t bt_stride,
+                         int64_t B, int64_t max_pages, float* k_out, float* v_out, int64_t L,
+                         void* stream);
+
+/* Decode attention of one query token per sequence over its cached tokens
+ * [0, seq_lens[b]): q [B, Hq, 128] (strides q_stride_b, q_stride_h), GQA with
+ * Hq / num_kv_heads <= 16 query heads per KV head, softmax scale sm_scale.
+ * Split-K over the pages (n_splits, 0 = chosen from the device size) with a
+ * log-sum-exp merge into out [B, Hq, 128] (strides out_stride_b,
+ * out_stride_h; dtype 0 fp16, 1 bf16, 2 fp32).  Workspace:
+ * exl3_kv_decode_workspace_size(B, Hq, num_kv_heads, max_pages, n_splits).
+ * Replaces q4_sparse_decode (the Triton _q4_decode_kernel and vLLM's split
+ * merge, src/vllm_exl3/minimax_q4kv_kernels.py:385-506, 772-877) for the
+ * dense int4 format above. */
+int64_t exl3_kv_decode_workspace_size(int64_t B, int64_t Hq, int64_t num_kv_heads,
+                                      int64_t max_pages, int64_t n_splits);
+int exl3_kv_decode(const void* q, int q_dtype, int64_t B, int64_t Hq, int64_t num_kv_heads,
+                   int64_t q_stride_b, int64_t q_stride_h, const uint8_t* pool, int64_t num_pages,
+                   const int32_t* block_table, int64_t bt_stride, int64_t max_pages,
+                   const int32_t* seq_lens, float sm_scale, void* out, int out_dtype,
+                   int64_t out_stride_b, int64_t out_stride_h, int64_t n_splits, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Instrumentation (no counterpart in the reference; used by the benchmark to
  * time individual kernels on their launch stream).  Between begin and end,
  * every instrumented call records HIP events at its phase boundaries:
@@ -163,6 +213,7 @@ int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hidden, int6
  *   exl3_moe_prefill: 0 route | 1 input rotation | 2 gate/up GEMMs | 3 activation
  *                     | 4 down GEMM | 5 combine
  *   exl3_fat_gemm{,_scatter}: 0 GEMM | 1 output rotation (+ scatter)
+ *   exl3_kv_decode:   0 split-K attention | 1 merge
  * Recording never synchronises.  exl3_profile_end waits for the events and
  * writes, per phase, the summed elapsed milliseconds over the recorded calls
  * (at most max_calls are recorded).  Not thread-safe. */

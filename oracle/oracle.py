@@ -315,3 +315,132 @@ def attention_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) 
     p /= p.sum(axis=-1, keepdims=True)
     o = np.einsum("bhgl,bhld->bhgd", p, v)
     return o.reshape(B, Hq, D)
+
+
+# ---------------------------------------------------------------------------
+# Paged int4 KV cache: page layout (format defined in this build)
+# ---------------------------------------------------------------------------
+# One page holds 16 tokens of one KV head in 2560 bytes (160 B per token):
+#   [   0, 1024)  K codes: token-major nibbles in the order the QK matrix-core
+#                 operand reads them (lane l = t + 16 j; 32-bit word g of the
+#                 lane's 16 bytes holds dims 32 g + 8 j + p at bits 4 p).
+#   [1024, 2048)  V codes: dim-major nibbles in the order the PV operand reads
+#                 them (lane l = m + 16 j for dims 16 b + m and tokens
+#                 4 j + i; word b // 2, bit 8 (b % 2) + (0, 16, 4, 20)[i]).
+#   [2048, 2176)  K scale fp16 [4 groups][16 tokens]
+#   [2176, 2304)  K zero  fp16 [4 groups][16 tokens]
+#   [2304, 2432)  V scale fp16 [4 groups][16 tokens]
+#   [2432, 2560)  V zero  fp16 [4 groups][16 tokens]
+# The pool is uint8 [num_pages, num_kv_heads, 2560]; a sequence's logical
+# page i lives at physical page block_table[b, i].
+
+KV_PAGE = 16
+KV_HEAD_DIM = 128
+KV_PAGE_BYTES = 2560
+KV_OFF_KS, KV_OFF_KZ, KV_OFF_VS, KV_OFF_VZ = 2048, 2176, 2304, 2432
+_V_BIT = (0, 16, 4, 20)
+
+
+def kv_k_nibble_bit(t: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """Bit offset (from the page start) of K code (token t, dim d)."""
+    t, d = np.asarray(t), np.asarray(d)
+    g, r = d // 32, d % 32
+    j, p = r // 8, r % 8
+    lane = t + 16 * j
+    return (16 * lane + 4 * g) * 8 + 4 * p
+
+
+def kv_v_nibble_bit(t: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """Bit offset (from the page start) of V code (token t, dim d)."""
+    t, d = np.asarray(t), np.asarray(d)
+    b, m = d // 16, d % 16
+    j, i = t // 4, t % 4
+    lane = m + 16 * j
+    return (1024 + 16 * lane + 4 * (b // 2)) * 8 + 8 * (b % 2) + np.asarray(_V_BIT)[i]
+
+
+def _put_nibbles(page: np.ndarray, bits: np.ndarray, codes: np.ndarray) -> None:
+    byte, sh = bits // 8, bits % 8
+    np.bitwise_or.at(page, byte.ravel(), (codes.astype(np.uint8) << sh.astype(np.uint8)).ravel())
+
+
+def _get_nibbles(page: np.ndarray, bits: np.ndarray) -> np.ndarray:
+    byte, sh = bits // 8, bits % 8
+    return (page[byte] >> sh.astype(np.uint8)) & 0xF
+
+
+def kv_pack_pages(k: np.ndarray, v: np.ndarray, seq_lens: np.ndarray, block_table: np.ndarray,
+                  num_pages: int) -> np.ndarray:
+    """Quantise K, V [B, Hkv, L, 128] into a paged pool [num_pages, Hkv, 2560].
+
+    Tokens at or past seq_lens[b] inside a sequence's last page are stored as
+    code 0 with scale 0 and zero 0; pages no sequence uses stay zero."""
+    k = np.asarray(k, dtype=np.float32)
+    v = np.asarray(v, dtype=np.float32)
+    B, Hkv, L, D = k.shape
+    assert D == KV_HEAD_DIM
+    pool = np.zeros((num_pages, Hkv, KV_PAGE_BYTES), dtype=np.uint8)
+    tt, dd = np.meshgrid(np.arange(KV_PAGE), np.arange(D), indexing="ij")
+    kbits, vbits = kv_k_nibble_bit(tt, dd), kv_v_nibble_bit(tt, dd)
+    for b in range(B):
+        n = int(seq_lens[b])
+        for lp in range((n + KV_PAGE - 1) // KV_PAGE):
+            pg = int(block_table[b, lp])
+            t0 = lp * KV_PAGE
+            cnt = min(KV_PAGE, n - t0)
+            for h in range(Hkv):
+                page = pool[pg, h]
+                for side, src, bits, off_s, off_z in ((0, k, kbits, KV_OFF_KS, KV_OFF_KZ),
+                                                      (1, v, vbits, KV_OFF_VS, KV_OFF_VZ)):
+                    rows = np.zeros((KV_PAGE, D), dtype=np.float32)
+                    rows[:cnt] = src[b, h, t0:t0 + cnt]
+                    q, s, z = kv_quantize_rows(rows)
+                    q[cnt:] = 0
+                    s[cnt:] = 0
+                    z[cnt:] = 0
+                    _put_nibbles(page, bits, q)
+                    page[off_s:off_s + 128] = np.ascontiguousarray(s.T).view(np.uint8).ravel()
+                    page[off_z:off_z + 128] = np.ascontiguousarray(z.T).view(np.uint8).ravel()
+    return pool
+
+
+def kv_unpack_page(page: np.ndarray, side: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """(codes uint8 [16, 128], scale fp16 [16, 4], zero fp16 [16, 4]) of one page side."""
+    tt, dd = np.meshgrid(np.arange(KV_PAGE), np.arange(KV_HEAD_DIM), indexing="ij")
+    bits = kv_k_nibble_bit(tt, dd) if side == 0 else kv_v_nibble_bit(tt, dd)
+    q = _get_nibbles(np.asarray(page, dtype=np.uint8), bits).astype(np.uint8)
+    off_s, off_z = (KV_OFF_KS, KV_OFF_KZ) if side == 0 else (KV_OFF_VS, KV_OFF_VZ)
+    s = np.ascontiguousarray(page[off_s:off_s + 128]).view(np.float16).reshape(4, KV_PAGE).T
+    z = np.ascontiguousarray(page[off_z:off_z + 128]).view(np.float16).reshape(4, KV_PAGE).T
+    return q, s, z
+
+
+def kv_unpack_pages(pool: np.ndarray, seq_lens: np.ndarray, block_table: np.ndarray,
+                    L: int) -> tuple[np.ndarray, np.ndarray]:
+    """Dequantised K, V [B, Hkv, L, 128] fp32 (zeros past seq_lens)."""
+    B = len(seq_lens)
+    Hkv = pool.shape[1]
+    out = [np.zeros((B, Hkv, L, KV_HEAD_DIM), dtype=np.float32) for _ in range(2)]
+    for b in range(B):
+        n = int(seq_lens[b])
+        for lp in range((n + KV_PAGE - 1) // KV_PAGE):
+            pg = int(block_table[b, lp])
+            t0 = lp * KV_PAGE
+            cnt = min(KV_PAGE, n - t0)
+            for h in range(Hkv):
+                for side in (0, 1):
+                    q, s, z = kv_unpack_page(pool[pg, h], side)
+                    x = kv_dequantize_rows(q, s, z)
+                    out[side][b, h, t0:t0 + cnt] = x[:cnt]
+    return out[0], out[1]
+
+
+def attention_decode_lens(q: np.ndarray, k: np.ndarray, v: np.ndarray, seq_lens: np.ndarray,
+                          scale: float) -> np.ndarray:
+    """``attention_decode`` with per-sequence lengths (keys [0, seq_lens[b]))."""
+    out = np.zeros(q.shape, dtype=np.float64)
+    for b in range(q.shape[0]):
+        n = int(seq_lens[b])
+        if n > 0:
+            out[b:b + 1] = attention_decode(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n], scale)
+    return out

@@ -176,3 +176,54 @@ def to_device(experts: list, device) -> dict:
     out["k_tables"] = tuple(torch.tensor(ks[p], dtype=torch.int8, device=device) for p in names)
     out["_store"] = store
     return out
+
+
+# ---------------------------------------------------------------------------
+# KV cache decode workload (int4 paged cache)
+# ---------------------------------------------------------------------------
+
+def kv_inputs(seed: int, B: int, Hkv: int, L: int, D: int = 128, outlier_frac: float = 0.02,
+              outlier_scale: float = 8.0):
+    """K, V [B, Hkv, L, D] bf16-rounded N(0,1) values (float32 arrays) with a
+    seeded ``outlier_frac`` of the channels of each head scaled by
+    ``outlier_scale``."""
+    g = rng(seed)
+    n_out = max(1, int(round(outlier_frac * D)))
+    out = []
+    for _ in range(2):
+        x = g.standard_normal((B, Hkv, L, D), dtype=np.float32)
+        for h in range(Hkv):
+            ch = g.choice(D, size=n_out, replace=False)
+            x[:, h, :, ch] *= np.float32(outlier_scale)
+        bits = x.view(np.uint32)
+        bits = ((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+        out.append(bits.view(np.float32))
+    return out[0], out[1]
+
+
+def block_table(seed: int, B: int, max_pages: int, num_pages: int | None = None) -> np.ndarray:
+    """A random page assignment: every logical page of every sequence gets a
+    distinct physical page (a seeded permutation of the pool)."""
+    num_pages = num_pages or B * max_pages
+    perm = rng(seed).permutation(num_pages)[:B * max_pages]
+    return perm.reshape(B, max_pages).astype(np.int32)
+
+
+def kv_inputs_device(seed: int, B: int, Hkv: int, L: int, device, D: int = 128,
+                     outlier_frac: float = 0.02, outlier_scale: float = 8.0):
+    """``kv_inputs`` generated on the device with torch's seeded generator
+    (for the full-size workload; bf16 tensors [B, Hkv, L, D])."""
+    import torch
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    n_out = max(1, int(round(outlier_frac * D)))
+    out = []
+    for _ in range(2):
+        x = torch.randn((B, Hkv, L, D), device=device, generator=gen, dtype=torch.float32)
+        sc = torch.ones((Hkv, D), device=device)
+        for h in range(Hkv):
+            ch = torch.randperm(D, device=device, generator=gen)[:n_out]
+            sc[h, ch] = outlier_scale
+        out.append((x * sc[None, :, None, :]).to(torch.bfloat16))
+    return out[0], out[1]
