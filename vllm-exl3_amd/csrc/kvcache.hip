@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace exl3 {
 namespace {
@@ -43,6 +44,7 @@ constexpr int kKvDim = 128;
 constexpr int kKvPageBytes = 2560;
 constexpr int kOffVQ = 1024, kOffKS = 2048, kOffKZ = 2176, kOffVS = 2304, kOffVZ = 2432;
 constexpr int kKvMaxGroup = 16;      // query heads per KV head (one MFMA column block)
+constexpr int kKvWaves = 8;          // waves per decode workgroup
 constexpr uint32_t kMagic = 0x64006400u;  // fp16 pair (1024, 1024)
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -247,6 +249,10 @@ __global__ __launch_bounds__(256) void kv_unpack_kernel(const uint8_t* pool, int
 // ---------------------------------------------------------------------------
 // Decode attention
 // ---------------------------------------------------------------------------
+struct CodeMasks {
+    uint32_t lo, hi, magic;
+};
+
 struct KvDecodeParams {
     const void* q;
     int q_dtype;
@@ -260,6 +266,7 @@ struct KvDecodeParams {
     const int* seq_lens;
     int B, Hq, Hkv, G, S, pps;
     float scale_log2;  // sm_scale * log2(e)
+    CodeMasks masks;   // 0x000F000F, 0x00F000F0, 0x64006400
     float* o_part;     // [S][B][Hq][128], normalised by the split's own sum
     float* lse_part;   // [S][B][Hq], log2 domain
 };
@@ -267,39 +274,54 @@ struct KvDecodeParams {
 struct PageRegs {
     u32x4 kq, vq;
     u32x2 ks[4], vs[4];
-    uint32_t ca;  // (K zero, K scale) of (group j, token n)
+    uint32_t zk, sk;  // K zero and K scale of (group j, token n), low 16 bits
     u32x2 vz;     // V zeros of group n (n < 4), tokens 4 j .. 4 j + 3
 };
 
-__device__ __forceinline__ void load_page(PageRegs& r, const uint8_t* base, int lane, int j, int n) {
-    r.kq = __builtin_nontemporal_load((gu4p)(base + 16 * lane));
-    r.vq = __builtin_nontemporal_load((gu4p)(base + kOffVQ + 16 * lane));
+// Per-lane byte offsets inside a page (constant over the page loop).
+struct PageOffsets {
+    int codes;  // 16 lane: K codes at +0, V codes at +1024
+    int scl;    // 8 j: K scales at +2048 + 32 g, V scales at +2304 + 32 g
+    int kzs;    // 32 j + 2 n: K zero at +2176, K scale at +2048
+    int vz;     // 32 min(n, 3) + 8 j: V zeros at +2432
+};
+
+// One page through a buffer resource whose base is the page: the address
+// arithmetic is scalar and out-of-page offsets would read 0.
+__device__ __forceinline__ void load_page(PageRegs& r, const uint8_t* base, const PageOffsets& o) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, kKvPageBytes, 0x00020000);
+    r.kq = __builtin_amdgcn_raw_buffer_load_b128(rs, o.codes, 0, 0);
+    r.vq = __builtin_amdgcn_raw_buffer_load_b128(rs, o.codes + kOffVQ, 0, 0);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        r.ks[g] = *reinterpret_cast<const u32x2*>(base + kOffKS + 2 * (16 * g + 4 * j));
-        r.vs[g] = *reinterpret_cast<const u32x2*>(base + kOffVS + 2 * (16 * g + 4 * j));
+        r.ks[g] = __builtin_amdgcn_raw_buffer_load_b64(rs, o.scl + kOffKS + 32 * g, 0, 0);
+        r.vs[g] = __builtin_amdgcn_raw_buffer_load_b64(rs, o.scl + kOffVS + 32 * g, 0, 0);
     }
-    const uint32_t zk = *reinterpret_cast<const uint16_t*>(base + kOffKZ + 2 * (16 * j + n));
-    const uint32_t sk = *reinterpret_cast<const uint16_t*>(base + kOffKS + 2 * (16 * j + n));
-    r.ca = zk | (sk << 16);
-    const int nz = n < 4 ? n : 0;
-    r.vz = *reinterpret_cast<const u32x2*>(base + kOffVZ + 2 * (16 * nz + 4 * j));
+    // kept apart until use: combining them here would wait on the loads
+    r.zk = __builtin_amdgcn_raw_buffer_load_b16(rs, o.kzs + kOffKZ, 0, 0);
+    r.sk = __builtin_amdgcn_raw_buffer_load_b16(rs, o.kzs + kOffKS, 0, 0);
+    r.vz = __builtin_amdgcn_raw_buffer_load_b64(rs, o.vz + kOffVZ, 0, 0);
 }
 
-__device__ __forceinline__ half8_t raw8(uint32_t w) {
+// Raw codes as fp16 pairs 1024 + n (or 1024 + 16 n for the upper nibble of a
+// byte): one v_bitop3_b32 (w & m) | (magic & ~m) per pair (truth table 0xE2
+// for operands a = w, b = m, c = magic).
+
+__device__ __forceinline__ half8_t raw8(uint32_t w, const CodeMasks& m) {
     const uint32_t w8 = w >> 8;
     u32x4 r;
-    r.x = (w & 0x000F000Fu) | kMagic;
-    r.y = (w & 0x00F000F0u) | kMagic;
-    r.z = (w8 & 0x000F000Fu) | kMagic;
-    r.w = (w8 & 0x00F000F0u) | kMagic;
+    r.x = __builtin_amdgcn_bitop3_b32(w, m.lo, m.magic, 0xE2);
+    r.y = __builtin_amdgcn_bitop3_b32(w, m.hi, m.magic, 0xE2);
+    r.z = __builtin_amdgcn_bitop3_b32(w8, m.lo, m.magic, 0xE2);
+    r.w = __builtin_amdgcn_bitop3_b32(w8, m.hi, m.magic, 0xE2);
     return __builtin_bit_cast(half8_t, r);
 }
 
-__device__ __forceinline__ half4_t raw4(uint32_t w) {
+__device__ __forceinline__ half4_t raw4(uint32_t w, const CodeMasks& m) {
     u32x2 r;
-    r.x = (w & 0x000F000Fu) | kMagic;
-    r.y = (w & 0x00F000F0u) | kMagic;
+    r.x = __builtin_amdgcn_bitop3_b32(w, m.lo, m.magic, 0xE2);
+    r.y = __builtin_amdgcn_bitop3_b32(w, m.hi, m.magic, 0xE2);
     return __builtin_bit_cast(half4_t, r);
 }
 
@@ -314,14 +336,54 @@ __device__ __forceinline__ void split_hi_lo(float x, half_t& hi, half_t& lo) {
     lo = f32_to_f16_rne(x - (float)hi);
 }
 
+// Cross-lane max over the four lane rows that share a lane index mod 16
+// (lanes n, n + 16, n + 32, n + 48): two gfx950 permlane swaps, no LDS.  The
+// swaps are written as instructions (the optimiser merges the builtins' two
+// results into one), each fenced by two wait states on both sides because the
+// hazard recogniser does not look inside inline assembly.
+__device__ __forceinline__ float rows_max(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    float c = fmaxf(a, b), d = c;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+    return fmaxf(c, d);
+}
+__device__ __forceinline__ float rows_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+// Eight consecutive query elements (dims d0 .. d0 + 7) widened exactly.
+__device__ __forceinline__ void load_q8(const void* q, int dtype, int64_t off, float v[8]) {
+    if (dtype == kKvF32Id) {
+        const float4_t a = *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(q) + off);
+        const float4_t b = *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(q) + off + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = a[e];
+            v[4 + e] = b[e];
+        }
+        return;
+    }
+    const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(q) + off);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t hb = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        v[e] = dtype == kKvF16Id ? (float)bits_to_half(hb) : __builtin_bit_cast(float, hb << 16);
+    }
+}
+
 template <int DEPTH>
-__global__ __launch_bounds__(256, 2) void kv_decode_kernel(KvDecodeParams p) {
+__global__ __launch_bounds__(64 * kKvWaves, 2) void kv_decode_kernel(KvDecodeParams p) {
     const int lane = threadIdx.x & 63, j = lane >> 4, n = lane & 15;
-    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (unit >= (int64_t)p.B * p.Hkv * p.S) return;
-    const int split = (int)(unit % p.S);
-    const int64_t bh = unit / p.S;
-    const int h = (int)(bh % p.Hkv), b = (int)(bh / p.Hkv);
+    // wave-uniform control: everything below the unit index lives in SGPRs
+    // KV head fastest: the waves of one workgroup read the heads of the same
+    // physical pages (contiguous in the pool) at about the same time
+    const int unit = __builtin_amdgcn_readfirstlane((int)blockIdx.x * kKvWaves + (int)(threadIdx.x >> 6));
+    if (unit >= p.B * p.Hkv * p.S) return;
+    const int h = unit % p.Hkv;
+    const int bs = unit / p.Hkv;
+    const int split = bs % p.S, b = bs / p.S;
     const int seq = p.seq_lens[b];
     const int npg = seq > 0 ? min((seq + kKvPage - 1) / kKvPage, p.max_pages) : 0;
     const int p0 = split * p.pps;
@@ -329,33 +391,30 @@ __global__ __launch_bounds__(256, 2) void kv_decode_kernel(KvDecodeParams p) {
     const int hq = h * p.G + n;
     const bool qvalid = n < p.G;
 
-    // ---- query operands: group g, lane group j holds dims 32 g + 8 j + perm[s]
+    // ---- query operands: group g, lane row j holds dims 32 g + 8 j + perm[s]
     half8_t qb[4];
     float qs[4], qc[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         float v[8];
+        if (qvalid) {
+            load_q8(p.q, p.q_dtype, (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + 32 * g + 8 * j, v);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            v[e] = qvalid ? load_f32(p.q, p.q_dtype, (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh +
-                                                         32 * g + 8 * j + e) * p.scale_log2
-                          : 0.0f;
+            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+        }
         constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
         float s_eff = 0.0f, s_raw = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const float f = (s & 2) ? 0.0625f : 1.0f;
-            const half_t hv = f32_to_f16_rne(v[perm[s]] * f);
+            const half_t hv = f32_to_f16_rne(v[perm[s]] * p.scale_log2 * f);
             qb[g][s] = hv;
             s_raw += (float)hv;          // coefficient of the 1024 offset
             s_eff += (float)hv / f;      // coefficient of the code value
         }
-        s_eff += __shfl_xor(s_eff, 16, 64);
-        s_raw += __shfl_xor(s_raw, 16, 64);
-        s_eff += __shfl_xor(s_eff, 32, 64);
-        s_raw += __shfl_xor(s_raw, 32, 64);
-        qs[g] = s_eff;
-        qc[g] = 1024.0f * s_raw;
+        qs[g] = rows_sum(s_eff);
+        qc[g] = 1024.0f * rows_sum(s_raw);
     }
     // correction operand: k-slots 4 g .. 4 g + 3 = (Qs_hi, Qs_lo, -C_hi, -C_lo) of group g = j
     half4_t cb;
@@ -377,27 +436,27 @@ __global__ __launch_bounds__(256, 2) void kv_decode_kernel(KvDecodeParams p) {
     float4_t accz = float4_t{0.f, 0.f, 0.f, 0.f};
     float m_used = -INFINITY;
     const float4_t zero4 = float4_t{0.f, 0.f, 0.f, 0.f};
-    const half4_t neg1024 = __builtin_bit_cast(half4_t, u32x2{0xE400E400u, 0xE400E400u});
+    const half8_t neg1024 =
+        __builtin_bit_cast(half8_t, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
     const half2_t sixteenth = half2_t{(half_t)0.0625f, (half_t)0.0625f};
     const int* bt = p.block_table + (int64_t)b * p.bt_stride;
     const uint8_t* hbase = p.pool + (int64_t)h * kKvPageBytes;
+    PageOffsets offs;
+    offs.codes = 16 * lane;
+    offs.scl = 8 * j;
+    offs.kzs = 32 * j + 2 * n;
+    offs.vz = 32 * min(n, 3) + 8 * j;
 
-    auto page_base = [&](int lp) {
-        int pg = bt[lp];
-        pg = min(max(pg, 0), p.num_pages - 1);
-        return hbase + (int64_t)pg * p.page_stride;
-    };
-
-    auto compute = [&](const PageRegs& r, int lp) {
-        // ---- QK^T per group, then scale fold and the zero/offset correction
+    // QK^T of one page, the scale fold and the zero/offset correction; with
+    // MASK, tokens at or past seq get -inf.
+    auto scores = [&](const PageRegs& r, int lp, float (&sv)[4], auto mask_tag) {
         float4_t d[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(raw8(r.kq[g]), qb[g], zero4, 0, 0, 0);
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(raw8(r.kq[g], p.masks), qb[g], zero4, 0, 0, 0);
         u32x2 cav;
-        cav.x = __builtin_amdgcn_perm(r.ca, r.ca, 0x01000100u);  // (zero, zero)
-        cav.y = __builtin_amdgcn_perm(r.ca, r.ca, 0x03020302u);  // (scale, scale)
+        cav.x = __builtin_amdgcn_perm(r.zk, r.zk, 0x01000100u);  // (zero, zero)
+        cav.y = __builtin_amdgcn_perm(r.sk, r.sk, 0x01000100u);  // (scale, scale)
         float4_t sc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, cav), cb, zero4, 0, 0, 0);
-        float sv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float x = sc[i];
@@ -406,12 +465,18 @@ __global__ __launch_bounds__(256, 2) void kv_decode_kernel(KvDecodeParams p) {
                 const uint32_t w = (i < 2) ? r.ks[g].x : r.ks[g].y;
                 x += ((i & 1) ? half_hi(w) : half_lo(w)) * d[g][i];
             }
-            sv[i] = (lp * kKvPage + 4 * j + i < seq) ? x : -INFINITY;
+            sv[i] = x;
         }
-        // ---- online softmax (log2 domain), lazy rescale by 2^8 steps
-        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if constexpr (decltype(mask_tag)::value) {
+            const int tok0 = lp * kKvPage + 4 * j;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (tok0 + i >= seq) sv[i] = -INFINITY;
+        }
+    };
+    // online softmax (log2 domain): rescale only when the running maximum has
+    // grown by more than 2^8 (one wave-uniform branch per group of pages)
+    auto rescale_to = [&](float mx) {
         if (__builtin_amdgcn_ballot_w64(mx > m_used + 8.0f)) {
             const float m_new = fmaxf(m_used, mx);
             const float alpha = m_used == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_used - m_new);
@@ -420,52 +485,121 @@ __global__ __launch_bounds__(256, 2) void kv_decode_kernel(KvDecodeParams p) {
             accz *= alpha;
             m_used = m_new;
         }
-        float pr[4];
+    };
+    // P V of two pages with 16x16x32 MFMAs (k = 8 j + 4 page + i).  Per group
+    // the B operand is s * P (upper-nibble tokens / 16); the offset
+    // correction -1024 * (s * P) goes into the same accumulators right after
+    // the product; one more MFMA of [zero rows | ones row] . P gives the
+    // zero-point term of every group and the softmax denominator.
+    auto pv2 = [&](const PageRegs& r0, const PageRegs& r1, const float (&s0)[4],
+                   const float (&s1)[4]) {
+        half2_t pp[2][2];
+        {
+            float pr[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(sv[i] - m_used);
-        const half2_t p01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(pr[0], pr[1]));
-        const half2_t p23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(pr[2], pr[3]));
-        const half2_t p23s = p23 * sixteenth;
-        // ---- P V: per group the B operand is s * P (upper-nibble tokens / 16)
-        half4_t bp[4];
+            for (int i = 0; i < 4; ++i) {
+                pr[i] = __builtin_amdgcn_exp2f(s0[i] - m_used);
+                pr[4 + i] = __builtin_amdgcn_exp2f(s1[i] - m_used);
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                pp[q][0] = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(pr[4 * q], pr[4 * q + 1]));
+                pp[q][1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(pr[4 * q + 2], pr[4 * q + 3]));
+            }
+        }
+        const half2_t p0s = pp[0][1] * sixteenth, p1s = pp[1][1] * sixteenth;
+        half8_t bp[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const half2_t lo = p01 * as_h2(r.vs[g].x);
-            const half2_t hi = p23s * as_h2(r.vs[g].y);
-            bp[g] = __builtin_bit_cast(half4_t, u32x2{as_u32(lo), as_u32(hi)});
+            u32x4 u;
+            u.x = as_u32(pp[0][0] * as_h2(r0.vs[g].x));
+            u.y = as_u32(p0s * as_h2(r0.vs[g].y));
+            u.z = as_u32(pp[1][0] * as_h2(r1.vs[g].x));
+            u.w = as_u32(p1s * as_h2(r1.vs[g].y));
+            bp[g] = __builtin_bit_cast(half8_t, u);
         }
 #pragma unroll
         for (int blk = 0; blk < 8; ++blk) {
-            const uint32_t w = r.vq[blk >> 1] >> (8 * (blk & 1));
-            acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(raw4(w), bp[blk >> 1], acc[blk], 0, 0, 0);
+            const int sh = 8 * (blk & 1);
+            const half4_t a0 = raw4(r0.vq[blk >> 1] >> sh, p.masks);
+            const half4_t a1 = raw4(r1.vq[blk >> 1] >> sh, p.masks);
+            const half8_t a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+            acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bp[blk >> 1], acc[blk], 0, 0, 0);
         }
 #pragma unroll
         for (int blk = 0; blk < 8; ++blk)
-            acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(neg1024, bp[blk >> 1], acc[blk], 0, 0, 0);
-        // zero-point term (rows 0..3 = groups) and the softmax denominator (row 4)
-        u32x2 za = r.vz;
-        if (n >= 4) za = (n == 4) ? u32x2{0x3C003C00u, 0x3C003C00u} : u32x2{0u, 0u};
-        const half4_t pb = __builtin_bit_cast(half4_t, u32x2{as_u32(p01), as_u32(p23)});
-        accz = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, za), pb, accz, 0, 0, 0);
+            acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg1024, bp[blk >> 1], acc[blk], 0, 0, 0);
+        u32x4 za = u32x4{r0.vz.x, r0.vz.y, r1.vz.x, r1.vz.y};
+        if (n >= 4) za = (n == 4) ? u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}
+                                  : u32x4{0u, 0u, 0u, 0u};
+        const half8_t pb = __builtin_bit_cast(
+            half8_t, u32x4{as_u32(pp[0][0]), as_u32(pp[0][1]), as_u32(pp[1][0]), as_u32(pp[1][1])});
+        accz = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, za), pb, accz, 0, 0, 0);
     };
+    using NoMask = std::integral_constant<bool, false>;
+    using Mask = std::integral_constant<bool, true>;
 
-    // ---- page loop, DEPTH pages in flight
+    // ---- page loop.  The block-table entries of up to 256 pages sit one per
+    // lane in four registers and are read with readlane; DEPTH pages are in
+    // flight and are consumed in pairs.  Loads are unconditional (prefetches
+    // past the chunk reload its last page), so the wait counts stay exact and
+    // the pipeline never drains inside a chunk.  Each pair of full pages
+    // shares one maximum and one rescale decision; the remaining (at most
+    // DEPTH) pages, including a partial last page, are masked, and a page past
+    // the chunk contributes nothing (all its scores are -inf).
+    static_assert(DEPTH % 2 == 0, "pages are consumed in pairs");
+    const int nfull = seq >> 4;
     PageRegs ring[DEPTH];
+    for (int c0 = p0; c0 < p1; c0 += 256) {
+        const int c1 = min(c0 + 256, p1);
+        const int cf = min(c1, nfull);
+        int btv[4];
 #pragma unroll
-    for (int dd = 0; dd < DEPTH; ++dd)
-        if (p0 + dd < p1) load_page(ring[dd], page_base(p0 + dd), lane, j, n);
-    int lp = p0;
-    for (; lp + DEPTH <= p1; lp += DEPTH) {
+        for (int k = 0; k < 4; ++k) {
+            const int e = c0 + 64 * k + lane;
+            const int v = e < c1 ? bt[e] : 0;
+            btv[k] = min(max(v, 0), p.num_pages - 1);
+        }
+        auto base_of = [&](int lp) {
+            const int k = min(lp, c1 - 1) - c0;
+            const int v = k < 64 ? btv[0] : k < 128 ? btv[1] : k < 192 ? btv[2] : btv[3];
+            const int pg = __builtin_amdgcn_readlane(v, k & 63);
+            return hbase + (int64_t)pg * p.page_stride;
+        };
 #pragma unroll
-        for (int dd = 0; dd < DEPTH; ++dd) {
-            const PageRegs cur = ring[dd];
-            if (lp + dd + DEPTH < p1) load_page(ring[dd], page_base(lp + dd + DEPTH), lane, j, n);
-            compute(cur, lp + dd);
+        for (int dd = 0; dd < DEPTH; ++dd) load_page(ring[dd], base_of(c0 + dd), offs);
+        int lp = c0;
+        for (; lp + DEPTH <= cf; lp += DEPTH) {
+#pragma unroll
+            for (int dd = 0; dd < DEPTH; dd += 2) {
+                float s0[4], s1[4];
+                scores(ring[dd], lp + dd, s0, NoMask{});
+                scores(ring[dd + 1], lp + dd + 1, s1, NoMask{});
+                const float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                       fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+                rescale_to(rows_max(mx));
+                pv2(ring[dd], ring[dd + 1], s0, s1);
+                load_page(ring[dd], base_of(lp + dd + DEPTH), offs);
+                load_page(ring[dd + 1], base_of(lp + dd + 1 + DEPTH), offs);
+            }
+        }
+#pragma unroll
+        for (int dd = 0; dd < DEPTH; dd += 2) {
+            if (lp + dd < c1) {
+                float s0[4], s1[4];
+                scores(ring[dd], lp + dd, s0, Mask{});
+                scores(ring[dd + 1], lp + dd + 1, s1, Mask{});
+                if (lp + dd + 1 >= c1) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s1[i] = -INFINITY;
+                }
+                const float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                       fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+                rescale_to(rows_max(mx));
+                pv2(ring[dd], ring[dd + 1], s0, s1);
+            }
         }
     }
-#pragma unroll
-    for (int dd = 0; dd < DEPTH; ++dd)
-        if (lp + dd < p1) compute(ring[dd], lp + dd);
 
     // ---- epilogue: zero-point term and denominator from the rows of accz
     float zt[4];
@@ -486,39 +620,63 @@ __global__ __launch_bounds__(256, 2) void kv_decode_kernel(KvDecodeParams p) {
     if (j == 0) p.lse_part[row] = lsum > 0.0f ? m_used + __log2f(lsum) : -INFINITY;
 }
 
-// One wave per (sequence, query head): out = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M).
+// out = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M), one wave per
+// (sequence, query head): lane s holds split s's log-sum-exp (S <= 64), lane
+// l accumulates dims 2 l, 2 l + 1; the partial rows are loaded 16 splits at a
+// time before they are weighted.
+constexpr int kKvMaxSplits = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
 __global__ __launch_bounds__(256) void kv_merge_kernel(const float* o_part, const float* lse_part,
                                                        int S, int B, int Hq, void* out,
                                                        int out_dtype, int64_t o_sb, int64_t o_sh) {
     const int lane = threadIdx.x & 63;
-    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (unit >= (int64_t)B * Hq) return;
-    const int hq = (int)(unit % Hq), b = (int)(unit / Hq);
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, lse_part[((int64_t)s * B + b) * Hq + hq]);
-    float a0 = 0.f, a1 = 0.f, wsum = 0.f;
-    if (M != -INFINITY) {
-        for (int s = 0; s < S; ++s) {
-            const int64_t row = ((int64_t)s * B + b) * Hq + hq;
-            const float l = lse_part[row];
-            if (l == -INFINITY) continue;
-            const float w = __builtin_amdgcn_exp2f(l - M);
-            wsum += w;
-            a0 += w * o_part[row * kKvDim + 2 * lane];
-            a1 += w * o_part[row * kKvDim + 2 * lane + 1];
+    const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+    if (row >= B * Hq) return;
+    const int hq = row % Hq, b = row / Hq;
+    const int64_t stride = (int64_t)B * Hq;
+    const float l = lane < S ? lse_part[lane * stride + row] : -INFINITY;
+    const float M = wave_max(l);
+    const float w = (M == -INFINITY || l == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(l - M);
+    const float wsum = wave_sum(w);
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    f2 acc = f2{0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += 16) {
+        f2 o[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            o[u] = s0 + u < S ? *reinterpret_cast<const f2*>(o_part + ((s0 + u) * stride + row) * kKvDim + 2 * lane)
+                              : f2{0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            if (s0 + u < S) {
+                const float ws = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s0 + u));
+                acc += ws * o[u];
+            }
         }
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.0f;
     const int64_t o = (int64_t)b * o_sb + (int64_t)hq * o_sh + 2 * lane;
-    store_f(out, out_dtype, o, a0 * inv);
-    store_f(out, out_dtype, o + 1, a1 * inv);
+    store_f(out, out_dtype, o, acc[0] * inv);
+    store_f(out, out_dtype, o + 1, acc[1] * inv);
 }
 
 int auto_splits(int64_t B, int64_t Hkv, int64_t max_pages) {
     const int64_t want = (2 * 4 * (int64_t)num_cus() + B * Hkv - 1) / (B * Hkv);
     int64_t s = 1;
     while (s < want) s <<= 1;
-    return (int)std::max<int64_t>(1, std::min<int64_t>(s, max_pages));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(s, kKvMaxSplits), max_pages));
 }
 
 }  // namespace
@@ -600,6 +758,7 @@ EXL3_API int exl3_kv_decode(const void* q, int q_dtype, int64_t B, int64_t Hq, i
                kKvMaxGroup);
     EXL3_CHECK(max_pages >= 1 && num_pages >= 1 && bt_stride >= max_pages && n_splits >= 0,
                "kv decode: invalid page geometry");
+    EXL3_CHECK(n_splits <= kKvMaxSplits, "kv decode supports at most %d splits", kKvMaxSplits);
     EXL3_CHECK(std::isfinite(sm_scale), "kv decode: sm_scale must be finite");
     EXL3_CHECK(B * Hq * max_pages < ((int64_t)1 << 31), "kv decode: problem too large");
     const int S = n_splits ? (int)std::min(n_splits, max_pages) : auto_splits(B, Hkv, max_pages);
@@ -626,12 +785,13 @@ EXL3_API int exl3_kv_decode(const void* q, int q_dtype, int64_t B, int64_t Hq, i
     p.S = S;
     p.pps = (int)((max_pages + S - 1) / S);
     p.scale_log2 = sm_scale * 1.4426950408889634f;
+    p.masks = CodeMasks{0x000F000Fu, 0x00F000F0u, kMagic};
     p.o_part = reinterpret_cast<float*>(workspace);
     p.lse_part = p.o_part + (int64_t)S * B * Hq * kKvDim;
     profile_begin_call();
     profile_mark(0, st);
     const int64_t units = B * Hkv * S;
-    kv_decode_kernel<2><<<(unsigned)((units + 3) / 4), 256, 0, st>>>(p);
+    kv_decode_kernel<4><<<(unsigned)((units + kKvWaves - 1) / kKvWaves), 64 * kKvWaves, 0, st>>>(p);
     EXL3_LAUNCHED();
     profile_mark(1, st);
     kv_merge_kernel<<<(unsigned)((B * Hq + 3) / 4), 256, 0, st>>>(p.o_part, p.lse_part, S, (int)B,
