@@ -40,18 +40,19 @@
 namespace exl3 {
 namespace {
 
-constexpr int kFatThreads = 256;
-constexpr int kTM = 256;        // rows per tile
-constexpr int kTN = 256;        // output columns per tile
-constexpr int kTK = 32;         // k per step (two tile rows)
-constexpr int kLdk = 40;        // fp16 per LDS row of A / B (32 + 8 pad)
-constexpr int kABytes = kTM * kLdk * 2;
-constexpr int kBBytes = kTN * kLdk * 2;
-constexpr int kTBytesMax = 1024 * 4;  // packed bytes per k-step at K <= 4
-constexpr int kFatLds = 3 * kABytes + 2 * kBBytes + 3 * kTBytesMax;
+constexpr int kFatThreads = 256;  // 4 waves; each stages, decodes and multiplies
+constexpr int kTM = 256;          // rows per tile
+constexpr int kTN = 256;          // output columns per tile
+constexpr int kTK = 32;           // k per step (two tile rows)
+constexpr int kABytes = kTM * kTK * 2;  // A stage: [256 rows][32 k] fp16, 64 B per row
+constexpr int kBBytes = kTN * kTK * 2;  // B stage: [256 cols][32 k] fp16, 64 B per column
+constexpr int kStages = 3;
+constexpr int kFatLds = kStages * (kABytes + kBBytes);  // 96 KB
+constexpr int kRing = 2;          // k-steps of global loads in flight (beyond the LDS lead)
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const v4u* gv4p;
+typedef __attribute__((address_space(1))) const uint32_t* gu32p;
 
 struct FatParams {
     // A: fp16 rows; row r of the tile is a + (a_row) * lda
@@ -132,24 +133,24 @@ struct PairGeom {
     static constexpr int shift(int b1, int b2, int p) { return 32 * (rel(b1, b2, p) + 1) - end(b1, b2, p); }
 };
 
-// Decode the 32 weights of group g of one staged tile into four B units.
+// Byte offset of 16-byte chunk c (8 k values) of row (or column) r in an A or
+// B stage: rows of 64 bytes, chunk index xor-ed with bits 2..3 of r and bits
+// 3..4 of r.  Any 16 rows starting at a multiple of 16 then cover all 64
+// banks at one chunk (the MFMA operand reads), and so do the stage writes
+// (four rows x four chunks for A; columns 16 tc + g (+ 8), tc in {0, 1},
+// g in 0..7 for the decoded B units).
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + (((c ^ (r >> 2) ^ (r >> 3)) & 3) << 4); }
+
+// Decode all 32 weights of group g of a tile from the group's K + 1 stream
+// words w[] (word F + j, F = g K - 1, wrapping) and store the four 8-k units
+// (one 16-byte MFMA operand fragment each): unit (b1, b2) is column
+// col0 + 8 b2, chunk c0 + b1 of the B stage.
 template <int K, int CB>
-__device__ __forceinline__ void decode_group(const uint8_t* tile, int g, uint16_t* bl, int n_base,
-                                             int k_base) {
-    constexpr int n32 = 8 * K;
-    constexpr int NW = K + 1;
-    uint32_t w[NW];
-    const uint32_t* tw = reinterpret_cast<const uint32_t*>(tile);
-    const int F = g * K - 1;
+__device__ __forceinline__ void decode_group(const uint32_t (&w)[K + 1], uint8_t* B, int col0, int c0) {
 #pragma unroll
-    for (int j = 0; j < NW; ++j) {
-        const int idx = F + j;
-        w[j] = tw[idx < 0 ? idx + n32 : idx];
-    }
+    for (int b2 = 0; b2 < 2; ++b2)
 #pragma unroll
-    for (int b1 = 0; b1 < 2; ++b1)
-#pragma unroll
-        for (int b2 = 0; b2 < 2; ++b2) {
+        for (int b1 = 0; b1 < 2; ++b1) {
             v4u u;
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
@@ -158,134 +159,162 @@ __device__ __forceinline__ void decode_group(const uint8_t* tile, int g, uint16_
                     __builtin_amdgcn_alignbit(w[rel - 1], w[rel], PairGeom<K>::shift(b1, b2, p));
                 u[p] = decode_pair<K, CB>(s);
             }
-            const int n = n_base + g + 8 * b2;
-            *reinterpret_cast<v4u*>(bl + n * kLdk + k_base + 8 * b1) = u;
+            *reinterpret_cast<v4u*>(B + swz(col0 + 8 * b2, c0 + b1)) = u;
         }
 }
 
-template <int CB, int K>
-__device__ __forceinline__ void fat_tile(const FatParams& p, uint8_t* lds, const uint8_t* trellis,
-                                         int64_t a_row0, int rows_valid, int64_t out_row0, int nt) {
-    uint16_t* Abuf = reinterpret_cast<uint16_t*>(lds);
-    uint16_t* Bbuf = reinterpret_cast<uint16_t*>(lds + 3 * kABytes);
-    uint8_t* Tbuf = lds + 3 * kABytes + 2 * kBBytes;
+// LDS-only barrier: the stage buffers are handed over through LDS, and the
+// global prefetches must stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+struct FatTile {
+    int64_t a_row0, out_row0;
+    int rows_valid, nt;
+    const uint8_t* trellis;
+};
+
+// One 256 x 256 output tile.  Wave w = (wm, wn) multiplies row fragments
+// wm, wm + 2, ..., (MF of them, 16 rows each) by column fragments
+// 8 wn .. 8 wn + 7.  Per k-step s every thread, in one basic block:
+//   * issues the MFMAs of step s (operands read during step s - 1),
+//   * reads the operand fragments of step s + 1 from LDS stage (s + 1) % 3,
+//   * stages step s + 2 into LDS stage (s + 2) % 3: four 16-byte A chunks
+//     and the decode of one trellis group (32 weights, four B units),
+//   * issues the global loads of step s + 2 + kRing,
+// and the wave scheduler interleaves the decode VALU work with the MFMAs.
+// One LDS-only barrier per k-step.
+template <int CB, int K, int MF>
+__device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, uint8_t* lds) {
     constexpr int tile_bytes = 32 * K;
-    constexpr int tbytes = 32 * tile_bytes;  // 2 tile rows x 16 tiles
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wm = w >> 1, wn = w & 1;
+    const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
     const int tiles_n = p.N >> 4;
-    const int n_cols = min(kTN, p.N - nt * kTN);      // 128 or 256
-    const int tcols = n_cols >> 4;                      // valid tile columns (8 or 16)
-    const int nsteps = p.K_in / kTK;
 
-    // ---- global loads of one k-step into registers
+    // ---- staging roles
+    const int ac = tid & 3, ar0 = tid >> 2;  // A: chunk ac of rows ar0 + 64 j
+    int64_t a_off[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+        a_off[jj] = (ft.a_row0 + min(ar0 + 64 * jj, ft.rows_valid - 1)) * p.lda + 8 * ac;
+    const int t_idx = tid >> 3, g = tid & 7;  // decode: group g of tile (tr, tc)
+    const int tr = t_idx >> 4, tc = t_idx & 15;
+    // a last tile of 128 columns: the upper half decodes a copy of the last
+    // valid tile column (in bounds; those B columns are never multiplied)
+    const int tcols = min(16, tiles_n - ft.nt * 16);
+    const uint32_t* tbase = reinterpret_cast<const uint32_t*>(
+        ft.trellis + ((size_t)tr * tiles_n + (size_t)ft.nt * 16 + min(tc, tcols - 1)) * tile_bytes);
+    const size_t step_words = (size_t)2 * tiles_n * tile_bytes / 4;
+    int widx[K + 1];
+#pragma unroll
+    for (int j = 0; j < K + 1; ++j) {
+        const int idx = g * K - 1 + j;
+        widx[j] = idx < 0 ? idx + 8 * K : idx;
+    }
+    const int col0 = tc * 16 + g;
+
+    // ---- operand fragment offsets (the swizzle key of a 16-row fragment
+    // depends on the parity of the fragment index)
+    const int x = lane & 15, kc = lane >> 4;
+    const int off_ev = swz(x, kc), off_od = swz(16 + x, kc) - 16 * 64;
+
     v4u ga[4];
-    v4u gt;
-    const int a_chunk = tid & 3;
-    auto load_step = [&](int s) {
-        const int k0 = s * kTK;
+    uint32_t gw[K + 1];
+    auto load = [&](int t) {
+        t = min(t, nsteps - 1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int r = (tid >> 2) + 64 * j;
-            r = min(r, rows_valid - 1);
-            ga[j] = __builtin_nontemporal_load(
-                (gv4p)(p.a + (a_row0 + r) * p.lda + k0 + a_chunk * 8));
-        }
-        const int off = tid * 16;
-        const int seg = off / (16 * tile_bytes);
-        const int in_seg = off - seg * 16 * tile_bytes;
-        if (off < tbytes && in_seg < tcols * tile_bytes) {
-            const uint8_t* src = trellis +
-                                 ((size_t)(2 * s + seg) * tiles_n + (size_t)nt * 16) * tile_bytes +
-                                 in_seg;
-            gt = __builtin_nontemporal_load((gv4p)src);
-        }
-    };
-    auto store_step = [&](int s) {
-        uint16_t* A = Abuf + (s % 3) * (kABytes / 2);
+        for (int jj = 0; jj < 4; ++jj)
+            ga[jj] = __builtin_nontemporal_load((gv4p)(p.a + a_off[jj] + t * kTK));
+        // global (not flat) loads: flat loads would also count against the
+        // LDS counter that every k-step barrier drains
+        const gu32p tw = (gu32p)(tbase + (size_t)t * step_words);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int r = (tid >> 2) + 64 * j;
-            *reinterpret_cast<v4u*>(A + r * kLdk + a_chunk * 8) = ga[j];
-        }
-        const int off = tid * 16;
-        const int seg = off / (16 * tile_bytes);
-        const int in_seg = off - seg * 16 * tile_bytes;
-        if (off < tbytes && in_seg < tcols * tile_bytes)
-            *reinterpret_cast<v4u*>(Tbuf + (s % 3) * kTBytesMax + off) = gt;
+        for (int j = 0; j < K + 1; ++j) gw[j] = __builtin_nontemporal_load(tw + widx[j]);
     };
-    // ---- decode of one k-step: thread -> (tile row, tile column, group)
-    const int d_sel = tid >> 7, d_col = (tid >> 3) & 15, d_g = tid & 7;
-    auto decode_step = [&](int s) {
-        if (d_col < tcols) {
-            const uint8_t* tile = Tbuf + (s % 3) * kTBytesMax + (d_sel * 16 + d_col) * tile_bytes;
-            decode_group<K, CB>(tile, d_g, Bbuf + (s & 1) * (kBBytes / 2), d_col * 16, d_sel * 16);
-        }
+    auto stage = [&](int t) {
+        const int st = t % kStages;
+        uint8_t* A = lds + st * kABytes;
+        uint8_t* B = lds + kStages * kABytes + st * kBBytes;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[jj];
+        decode_group<K, CB>(gw, B, col0, 2 * tr);
     };
 
-    float4_t acc[8][8];
+    constexpr int MFA = MF > 0 ? MF : 1;
+    float4_t acc[MFA][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < MFA; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-    const int m_rows = rows_valid - wm * 128;
-    const int mf_valid = m_rows <= 0 ? 0 : min(8, (m_rows + 15) >> 4);
-    const bool wave_on = (wn * 128 < n_cols) && mf_valid > 0;
+    half8_t fa[MFA], fb[8];
+    auto read = [&](int t) {
+        const int st = t % kStages;
+        const uint8_t* A = lds + st * kABytes;
+        const uint8_t* B = lds + kStages * kABytes + st * kBBytes;
+#pragma unroll
+        for (int nf = 0; nf < 8; ++nf) {
+            const int f = 8 * wn + nf;
+            fb[nf] = *reinterpret_cast<const half8_t*>(B + f * 1024 + ((f & 1) ? off_od : off_ev));
+        }
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+            const int f = wm + 2 * i;
+            fa[i] = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
+        }
+    };
 
-    // ---- prologue: steps 0 and 1 staged, step 0 decoded
-    load_step(0);
-    store_step(0);
-    if (nsteps > 1) {
-        load_step(1);
-        store_step(1);
-    }
-    __syncthreads();
-    decode_step(0);
-    __syncthreads();
+    // ---- prologue: stage steps 0 and 1, registers hold step 2
+    load(0);
+    stage(0);
+    load(1);
+    stage(1);
+    load(2);
+    lds_barrier();
 
-    const int frag_k = 8 * (lane >> 4);
+    // ---- main loop: one k-step per iteration.  The operand reads of step s
+    // and the staging of step s + 2 (A copy + trellis decode) are independent
+    // of each other and of the MFMAs' accumulators, so the decode VALU work
+    // hides the LDS read latency and runs beside the MFMAs.
     for (int s = 0; s < nsteps; ++s) {
-        const bool pre = s + 2 < nsteps;
-        if (pre) load_step(s + 2);
-        if (s + 1 < nsteps) decode_step(s + 1);
-        if (wave_on) {
-            const uint16_t* A = Abuf + (s % 3) * (kABytes / 2);
-            const uint16_t* B = Bbuf + (s & 1) * (kBBytes / 2);
-            half8_t bf[8];
+        if constexpr (MF > 0) read(s);
+        stage(s + 2);
+        load(s + 3);
+        if constexpr (MF > 0) {
 #pragma unroll
-            for (int nf = 0; nf < 8; ++nf)
-                bf[nf] = *reinterpret_cast<const half8_t*>(
-                    B + (wn * 128 + nf * 16 + (lane & 15)) * kLdk + frag_k);
+            for (int i = 0; i < MF; ++i)
 #pragma unroll
-            for (int mf = 0; mf < 8; ++mf) {
-                if (mf < mf_valid) {
-                    const half8_t af = *reinterpret_cast<const half8_t*>(
-                        A + (wm * 128 + mf * 16 + (lane & 15)) * kLdk + frag_k);
+                for (int nf = 0; nf < 8; ++nf)
+                    acc[i][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[nf], acc[i][nf], 0, 0, 0);
+            // issue order: the operand reads first, then every MFMA followed
+            // by a few VALU ops of the decode, so the matrix core and the
+            // VALU work side by side
+            __builtin_amdgcn_sched_group_barrier(0x100, 8 + MF, 0);  // DS read
 #pragma unroll
-                    for (int nf = 0; nf < 8; ++nf)
-                        acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nf], acc[mf][nf],
-                                                                             0, 0, 0);
-                }
+            for (int i = 0; i < 8 * MF; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
             }
         }
-        if (pre) store_step(s + 2);
-        __syncthreads();
+        lds_barrier();
     }
 
-    // ---- epilogue: Z * out_scale
-    if (!wave_on) return;
-    const int col0 = nt * kTN + wn * 128 + (lane & 15);
+    // ---- epilogue: Z * out_scale for the valid rows
+    if constexpr (MF > 0) {
+        const int colw = ft.nt * kTN + 128 * wn + (lane & 15);
 #pragma unroll
-    for (int mf = 0; mf < 8; ++mf) {
-        if (mf < mf_valid) {
+        for (int i = 0; i < MF; ++i) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = wm * 128 + mf * 16 + 4 * (lane >> 4) + i;
-                if (r < rows_valid) {
-                    const int64_t o = (out_row0 + r) * p.ldo + col0;
+            for (int e = 0; e < 4; ++e) {
+                const int r = 16 * (wm + 2 * i) + 4 * (lane >> 4) + e;
+                if (r < ft.rows_valid) {
+                    const int64_t o = (ft.out_row0 + r) * p.ldo + colw;
 #pragma unroll
                     for (int nf = 0; nf < 8; ++nf) {
-                        const float v = acc[mf][nf][i] * p.out_scale;
+                        const float v = acc[i][nf][e] * p.out_scale;
                         if (p.out_f32)
                             reinterpret_cast<float*>(p.out)[o + nf * 16] = v;
                         else
@@ -295,6 +324,26 @@ __device__ __forceinline__ void fat_tile(const FatParams& p, uint8_t* lds, const
             }
         }
     }
+}
+
+template <int CB, int K>
+__device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft, uint8_t* lds) {
+    // row fragments of this wave holding valid rows (wave row half wm takes
+    // fragments wm, wm + 2, ...), rounded up to 0, 1, 2, 4 or 8
+    const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
+    const int nfr = (ft.rows_valid + 15) >> 4;
+    const bool cols_ok = wn * 128 < p.N - ft.nt * kTN;  // a last tile may hold 128 columns
+    const int mine = (nfr > wm && cols_ok) ? (nfr - wm + 1) >> 1 : 0;
+    if (mine == 0)
+        fat_tile<CB, K, 0>(p, ft, lds);
+    else if (mine == 1)
+        fat_tile<CB, K, 1>(p, ft, lds);
+    else if (mine == 2)
+        fat_tile<CB, K, 2>(p, ft, lds);
+    else if (mine <= 4)
+        fat_tile<CB, K, 4>(p, ft, lds);
+    else
+        fat_tile<CB, K, 8>(p, ft, lds);
 }
 
 template <int CB>
@@ -307,31 +356,31 @@ __global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(1, 
     const int per = (G + 7) >> 3;
     const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if (logical >= G) return;
-    const int mt = logical / p.n_ntiles, nt = logical % p.n_ntiles;
-    int64_t a_row0, out_row0;
-    int rows_valid, K;
-    const uint8_t* trellis;
+    const int mt = logical / p.n_ntiles;
+    FatTile ft;
+    ft.nt = logical % p.n_ntiles;
+    int K;
     if (p.grouped) {
         if (mt >= *p.n_mtiles) return;
         const int slot = p.mt_slot[mt];
         const int row0 = p.mt_row0[mt];
         const int e = p.slot_expert[slot];
-        a_row0 = (int64_t)p.slot_start[slot] + row0;
-        out_row0 = a_row0;
-        rows_valid = min(kTM, p.slot_rows[slot] - row0);
-        trellis = reinterpret_cast<const uint8_t*>(p.trellis_tab[e]);
+        ft.a_row0 = (int64_t)p.slot_start[slot] + row0;
+        ft.out_row0 = ft.a_row0;
+        ft.rows_valid = min(kTM, p.slot_rows[slot] - row0);
+        ft.trellis = reinterpret_cast<const uint8_t*>(p.trellis_tab[e]);
         K = p.ktab ? (int)p.ktab[e] : p.kuni;
     } else {
-        a_row0 = (int64_t)mt * kTM;
-        out_row0 = a_row0;
-        rows_valid = min(kTM, p.M - mt * kTM);
-        trellis = p.trellis;
+        ft.a_row0 = (int64_t)mt * kTM;
+        ft.out_row0 = ft.a_row0;
+        ft.rows_valid = min(kTM, p.M - mt * kTM);
+        ft.trellis = p.trellis;
         K = p.kuni;
     }
     switch (K) {
-        case 2: fat_tile<CB, 2>(p, lds, trellis, a_row0, rows_valid, out_row0, nt); break;
-        case 3: fat_tile<CB, 3>(p, lds, trellis, a_row0, rows_valid, out_row0, nt); break;
-        case 4: fat_tile<CB, 4>(p, lds, trellis, a_row0, rows_valid, out_row0, nt); break;
+        case 2: fat_tile_k<CB, 2>(p, ft, lds); break;
+        case 3: fat_tile_k<CB, 3>(p, ft, lds); break;
+        case 4: fat_tile_k<CB, 4>(p, ft, lds); break;
         default: break;  // rejected on the host
     }
 }
