@@ -19,11 +19,13 @@
 // produces are eight consecutive k of one column: exactly one MFMA B-operand
 // lane fragment, stored with one ds_write_b128.
 //
-// Pipeline (one barrier per k-step): global loads of A rows and packed bits
-// run two k-steps ahead (3 LDS buffers), the decode of step s+1 is issued in
-// the same basic block as the MFMAs of step s so the scheduler can overlap
-// VALU decode with matrix-core work.  Waves whose 128-row slice holds no rows
-// of the expert skip their MFMAs but still share the decode.
+// Pipeline (one barrier per k-step, two LDS stages): global loads of A rows
+// and packed bits run kLoadSets k-steps ahead of their staging, the operand
+// fragments of step s+1 are read from LDS while the MFMAs of step s run, and
+// the decode of step s+2 is issued in the same basic block as those MFMAs so
+// the scheduler can overlap VALU decode with matrix-core work.  Waves whose
+// 128-row slice holds no rows of the expert skip their MFMAs but still share
+// the decode.
 //
 // The output rotation is not done in the GEMM epilogue: the GEMM stores
 // Z / sqrt(128) (Z = A x Wq) and the consumer kernel - the activation kernel,
@@ -46,9 +48,9 @@ constexpr int kTN = 256;          // output columns per tile
 constexpr int kTK = 32;           // k per step (two tile rows)
 constexpr int kABytes = kTM * kTK * 2;  // A stage: [256 rows][32 k] fp16, 64 B per row
 constexpr int kBBytes = kTN * kTK * 2;  // B stage: [256 cols][32 k] fp16, 64 B per column
-constexpr int kStages = 3;
-constexpr int kFatLds = kStages * (kABytes + kBBytes);  // 96 KB
-constexpr int kRing = 2;          // k-steps of global loads in flight (beyond the LDS lead)
+constexpr int kStages = 2;
+constexpr int kLoadSets = 2;      // k-steps of global loads in flight, in registers
+constexpr int kFatLds = kStages * (kABytes + kBBytes);  // 64 KB
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const v4u* gv4p;
@@ -179,14 +181,18 @@ struct FatTile {
 
 // One 256 x 256 output tile.  Wave w = (wm, wn) multiplies row fragments
 // wm, wm + 2, ..., (MF of them, 16 rows each) by column fragments
-// 8 wn .. 8 wn + 7.  Per k-step s every thread, in one basic block:
-//   * issues the MFMAs of step s (operands read during step s - 1),
-//   * reads the operand fragments of step s + 1 from LDS stage (s + 1) % 3,
-//   * stages step s + 2 into LDS stage (s + 2) % 3: four 16-byte A chunks
-//     and the decode of one trellis group (32 weights, four B units),
-//   * issues the global loads of step s + 2 + kRing,
-// and the wave scheduler interleaves the decode VALU work with the MFMAs.
-// One LDS-only barrier per k-step.
+// 8 wn .. 8 wn + 7.  k-step t lives in LDS stage t & 1 and in global-load
+// register set t % kLoadSets.  Iteration s, in one basic block:
+//   * reads the operand fragments of step s + 1 (LDS stage (s + 1) & 1),
+//   * stages step s + 2 into LDS stage s & 1 from its register set: four
+//     16-byte A chunks and the decode of one trellis group (32 weights,
+//     four B units),
+//   * issues the global loads of step s + 2 + kLoadSets into that set,
+//   * issues the MFMAs of step s on the operands read in iteration s - 1,
+// and the scheduler spreads the decode VALU work between the MFMAs.  The
+// LDS-only barrier at the end of the iteration also waits for this wave's
+// reads of step s + 1, so stage s & 1 is free for step s + 3 ... and the
+// operands are in registers when the next iteration's MFMAs issue.
 template <int CB, int K, int MF>
 __device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, uint8_t* lds) {
     constexpr int tile_bytes = 32 * K;
@@ -195,53 +201,49 @@ __device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, 
     const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
     const int tiles_n = p.N >> 4;
 
-    // ---- staging roles
+    // ---- staging roles.  Global loads go through buffer resources whose
+    // base is wave-uniform; the per-step advance is the scalar offset.
     const int ac = tid & 3, ar0 = tid >> 2;  // A: chunk ac of rows ar0 + 64 j
-    int64_t a_off[4];
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.a + ft.a_row0 * p.lda), (short)0, 0x7FFFFFFF, 0x00020000);
+    int a_voff[4];
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
-        a_off[jj] = (ft.a_row0 + min(ar0 + 64 * jj, ft.rows_valid - 1)) * p.lda + 8 * ac;
+        a_voff[jj] = (int)((min(ar0 + 64 * jj, ft.rows_valid - 1) * p.lda + 8 * ac) * 2);
     const int t_idx = tid >> 3, g = tid & 7;  // decode: group g of tile (tr, tc)
     const int tr = t_idx >> 4, tc = t_idx & 15;
     // a last tile of 128 columns: the upper half decodes a copy of the last
     // valid tile column (in bounds; those B columns are never multiplied)
     const int tcols = min(16, tiles_n - ft.nt * 16);
-    const uint32_t* tbase = reinterpret_cast<const uint32_t*>(
-        ft.trellis + ((size_t)tr * tiles_n + (size_t)ft.nt * 16 + min(tc, tcols - 1)) * tile_bytes);
-    const size_t step_words = (size_t)2 * tiles_n * tile_bytes / 4;
-    int widx[K + 1];
+    const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(ft.trellis + (size_t)ft.nt * 16 * tile_bytes), (short)0, 0x7FFFFFFF, 0x00020000);
+    const int t_voff = (tr * tiles_n + min(tc, tcols - 1)) * tile_bytes;
+    const int step_bytes = 2 * tiles_n * tile_bytes;
+    int w_voff[K + 1];
 #pragma unroll
     for (int j = 0; j < K + 1; ++j) {
         const int idx = g * K - 1 + j;
-        widx[j] = idx < 0 ? idx + 8 * K : idx;
+        w_voff[j] = t_voff + 4 * (idx < 0 ? idx + 8 * K : idx);
     }
     const int col0 = tc * 16 + g;
 
-    // ---- operand fragment offsets (the swizzle key of a 16-row fragment
-    // depends on the parity of the fragment index)
-    const int x = lane & 15, kc = lane >> 4;
-    const int off_ev = swz(x, kc), off_od = swz(16 + x, kc) - 16 * 64;
-
-    v4u ga[4];
-    uint32_t gw[K + 1];
-    auto load = [&](int t) {
-        t = min(t, nsteps - 1);
+    v4u ga[kLoadSets][4];
+    uint32_t gw[kLoadSets][K + 1];
+    auto load = [&](int t, int r) {
+        const int so = min(t, nsteps - 1);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj)
-            ga[jj] = __builtin_nontemporal_load((gv4p)(p.a + a_off[jj] + t * kTK));
-        // global (not flat) loads: flat loads would also count against the
-        // LDS counter that every k-step barrier drains
-        const gu32p tw = (gu32p)(tbase + (size_t)t * step_words);
+            ga[r][jj] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff[jj], so * (kTK * 2), 0));
 #pragma unroll
-        for (int j = 0; j < K + 1; ++j) gw[j] = __builtin_nontemporal_load(tw + widx[j]);
+        for (int j = 0; j < K + 1; ++j)
+            gw[r][j] = __builtin_amdgcn_raw_buffer_load_b32(trs, w_voff[j], so * step_bytes, 0);
     };
-    auto stage = [&](int t) {
-        const int st = t % kStages;
+    auto stage = [&](int st, int r) {
         uint8_t* A = lds + st * kABytes;
         uint8_t* B = lds + kStages * kABytes + st * kBBytes;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[jj];
-        decode_group<K, CB>(gw, B, col0, 2 * tr);
+        for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[r][jj];
+        decode_group<K, CB>(gw[r], B, col0, 2 * tr);
     };
 
     constexpr int MFA = MF > 0 ? MF : 1;
@@ -250,56 +252,66 @@ __device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, 
     for (int i = 0; i < MFA; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-    half8_t fa[MFA], fb[8];
-    auto read = [&](int t) {
-        const int st = t % kStages;
+    half8_t fa[2][MFA], fb[2][8];
+    // operand fragment offsets (the swizzle key of a 16-row fragment depends
+    // on the parity of the fragment index)
+    const int off_ev = swz(lane & 15, lane >> 4), off_od = swz(16 + (lane & 15), lane >> 4) - 16 * 64;
+    auto read = [&](int st, int o) {
         const uint8_t* A = lds + st * kABytes;
         const uint8_t* B = lds + kStages * kABytes + st * kBBytes;
 #pragma unroll
         for (int nf = 0; nf < 8; ++nf) {
             const int f = 8 * wn + nf;
-            fb[nf] = *reinterpret_cast<const half8_t*>(B + f * 1024 + ((f & 1) ? off_od : off_ev));
+            fb[o][nf] = *reinterpret_cast<const half8_t*>(B + f * 1024 + ((f & 1) ? off_od : off_ev));
         }
 #pragma unroll
         for (int i = 0; i < MF; ++i) {
             const int f = wm + 2 * i;
-            fa[i] = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
+            fa[o][i] = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
+        }
+    };
+    auto mma = [&](int o) {
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int nf = 0; nf < 8; ++nf)
+                acc[i][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[o][i], fb[o][nf], acc[i][nf], 0, 0, 0);
+        // issue order: the operand reads first, then every MFMA followed by
+        // a few VALU ops of the decode, so the matrix core and the VALU work
+        // side by side
+        __builtin_amdgcn_sched_group_barrier(0x100, 8 + MF, 0);  // DS read
+#pragma unroll
+        for (int i = 0; i < 8 * MF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
         }
     };
 
-    // ---- prologue: stage steps 0 and 1, registers hold step 2
-    load(0);
-    stage(0);
-    load(1);
-    stage(1);
-    load(2);
+    // ---- prologue: stages 0 and 1 hold steps 0 and 1, register sets hold
+    // steps 2 .. kLoadSets + 1, operand set 0 holds step 0.  The second
+    // barrier lets every wave finish reading stage 0 before step 2
+    // overwrites it.
+    load(0, 0);
+    load(1, 1);
+    stage(0, 0);
+    stage(1, 1);
+#pragma unroll
+    for (int t = 2; t < kLoadSets + 2; ++t) load(t, t % kLoadSets);
+    lds_barrier();
+    if constexpr (MF > 0) read(0, 0);
     lds_barrier();
 
-    // ---- main loop: one k-step per iteration.  The operand reads of step s
-    // and the staging of step s + 2 (A copy + trellis decode) are independent
-    // of each other and of the MFMAs' accumulators, so the decode VALU work
-    // hides the LDS read latency and runs beside the MFMAs.
-    for (int s = 0; s < nsteps; ++s) {
-        if constexpr (MF > 0) read(s);
-        stage(s + 2);
-        load(s + 3);
-        if constexpr (MF > 0) {
+    // ---- main loop, kLoadSets k-steps per trip (nsteps is a multiple of 4)
+    for (int s = 0; s < nsteps; s += kLoadSets) {
 #pragma unroll
-            for (int i = 0; i < MF; ++i)
-#pragma unroll
-                for (int nf = 0; nf < 8; ++nf)
-                    acc[i][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[nf], acc[i][nf], 0, 0, 0);
-            // issue order: the operand reads first, then every MFMA followed
-            // by a few VALU ops of the decode, so the matrix core and the
-            // VALU work side by side
-            __builtin_amdgcn_sched_group_barrier(0x100, 8 + MF, 0);  // DS read
-#pragma unroll
-            for (int i = 0; i < 8 * MF; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-            }
+        for (int u = 0; u < kLoadSets; ++u) {
+            const int r = (u + 2) % kLoadSets;  // register set of step s + u + 2
+            if constexpr (MF > 0) read((u + 1) & 1, (u + 1) & 1);
+            stage(u & 1, r);
+            load(s + u + 2 + kLoadSets, r);
+            if constexpr (MF > 0) mma(u & 1);
+            lds_barrier();
         }
-        lds_barrier();
     }
 
     // ---- epilogue: Z * out_scale for the valid rows
