@@ -52,6 +52,8 @@ def cpu_model() -> str:
 
 
 def run_batch(C, S, torch, layer, T, steps, warmup, dev, PhaseTimer):
+    from vllm_exl3_amd.profiling import MOE_PHASES
+
     x = torch.from_numpy(S.activations(10 + T, T, H)).to(dev).bfloat16()
     ids_np, w_np = S.softmax_topk(20 + T, T, E, TOPK)
     U = len(set(ids_np.ravel().tolist()))
@@ -62,24 +64,16 @@ def run_batch(C, S, torch, layer, T, steps, warmup, dev, PhaseTimer):
     def step():
         C.moe_forward(x, ids, w, layer, E, I, K=(K, K, K), codebook=CB, out=out)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    with PhaseTimer(max_calls=steps) as pt:
-        start.record()
-        for _ in range(steps):
-            step()
-        end.record()
-        torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    eager_ms, _ = time_steps(torch, step, steps, warmup)
+    ms = graph_time(torch, step, steps, warmup)
+    _, pt = time_steps(torch, step, steps, 1, PhaseTimer)
     step_bytes = U * EXPERT_BYTES + 2 * T * H + 4 * T * H
     gu_bytes = U * 2 * (H * I * K // 8 + 2 * (H + I)) + 2 * T * H  # gate+up trellis, scales, x
-    gu_ms = pt.mean_ms(1)
+    gu_ms = pt.mean_ms(MOE_PHASES.index("gate_up"))
     return {
         "T": T, "distinct_experts": U, "us_per_step": ms * 1e3, "gbs": step_bytes / (ms * 1e-3) / 1e9,
-        "phase_us": {n: pt.mean_ms(i) * 1e3 for i, n in enumerate(("route", "gate_up", "down", "combine"))},
+        "eager_us_per_step": eager_ms * 1e3,
+        "phase_us": {n: pt.mean_ms(i) * 1e3 for i, n in enumerate(MOE_PHASES)},
         "gate_up_bytes": gu_bytes, "gate_up_gbs": gu_bytes / (gu_ms * 1e-3) / 1e9,
         "ids": ids_np, "x": x,
     }
@@ -156,6 +150,30 @@ def time_steps(torch, fn, steps, warmup, PhaseTimer=None):
     return start.elapsed_time(end) / steps, pt
 
 
+def graph_time(torch, fn, steps, warmup):
+    """Milliseconds per call of fn replayed from a HIP graph: every kernel of
+    the step runs on every replay, only the host launch overhead is gone (a
+    serving decode loop replays captured steps the same way)."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del g
+    return ms
+
+
 def prefill_c2(C, S, torch, dev, steps, warmup, PhaseTimer):
     """Config 2: routed-MoE prefill, E128 top-8, H4096, I1024, K4 MCG,
     T=2048 tokens with Zipf(1.1) expert popularity."""
@@ -196,6 +214,8 @@ def decode_c3(C, S, torch, dev, steps, warmup, PhaseTimer):
     """Config 3: mixed-K routed-MoE decode, 256 routed experts (40/40/20
     K2/K3/K4, MCG) + 1 shared K4 expert (routed as a ninth slot of weight 1),
     top-8, H6144, I2048, T=64 uniform softmax routing."""
+    from vllm_exl3_amd.profiling import MOE_PHASES
+
     E3, H3, I3, T3 = 256, 6144, 2048, 64
     ks = S.mixed_k(3, E3) + [4]
     layer3 = S.moe_layer_device(3, E3 + 1, H3, I3, ks, dev)
@@ -211,7 +231,9 @@ def decode_c3(C, S, torch, dev, steps, warmup, PhaseTimer):
         C.moe_forward(x, ids, w, layer3, E3 + 1, I3, K=(4, 4, 4), k_tables=layer3["k_tables"],
                       codebook=1, out=out)
 
-    ms, pt = time_steps(torch, step, steps, warmup, PhaseTimer)
+    eager_ms, _ = time_steps(torch, step, steps, warmup)
+    ms = graph_time(torch, step, steps, warmup)
+    _, pt = time_steps(torch, step, steps, 1, PhaseTimer)
     used = sorted(set(ids_np.ravel().tolist()))
     nbytes = sum(ks[e] * 3 * H3 * I3 // 8 + 6 * (H3 + I3) for e in used) + 2 * T3 * H3 + 4 * T3 * H3
     del layer3
@@ -219,12 +241,14 @@ def decode_c3(C, S, torch, dev, steps, warmup, PhaseTimer):
         "workload": f"C3 mixed-K MoE decode, E{E3}+1 shared, top-{TOPK}, H{H3} I{I3}, "
                     f"K2/K3/K4 40/40/20 MCG, T={T3}",
         "us_per_step": round(ms * 1e3, 2),
+        "eager_us_per_step": round(eager_ms * 1e3, 2),
+        "timing": "HIP graph replay of the whole layer step; eager launches also reported",
         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_step": nbytes,
         "distinct_experts": len(used),
         "phase_us": {n: round(pt.mean_ms(i) * 1e3, 2)
-                     for i, n in enumerate(("route", "gate_up", "down", "combine"))},
+                     for i, n in enumerate(MOE_PHASES)},
     }
 
 
@@ -237,10 +261,14 @@ def linear_c0(C, S, torch, dev, steps, warmup):
     res = {}
     for m in (1, 16):
         x = torch.from_numpy(S.activations(100 + m, m, 2048)).to(dev).half()
-        ms, _ = time_steps(torch, lambda: C.exl3_gemm(x, t, su, sv, 4, True), steps, warmup)
+        fn = lambda: C.exl3_gemm(x, t, su, sv, 4, True)  # noqa: E731
+        eager_ms, _ = time_steps(torch, fn, steps, warmup)
+        ms = graph_time(torch, fn, steps, warmup)
         nbytes = 2048 * 2048 * 4 // 8 + 2 * 4096 + 2 * m * 4096
-        res[f"m={m}"] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-    return {"workload": "C0 EXL3 linear 2048x2048, K4 MCG, fp16 x", **res}
+        res[f"m={m}"] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "eager_us": round(eager_ms * 1e3, 2)}
+    return {"workload": "C0 EXL3 linear 2048x2048, K4 MCG, fp16 x",
+            "timing": "HIP graph replay (rotate, GEMV, finish); eager launches also reported", **res}
 
 
 def kv_decode_c4(S, torch, dev, steps, warmup, PhaseTimer):
@@ -334,6 +362,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic",
+        "timing": "HIP graph replay of the whole layer step (route, rotate, gate/up, act, down, "
+                  "combine); per-phase kernel times from a separate eager pass",
         "config": {
             "workload": f"C1 routed-MoE decode layer, E64 top-8, H2048 I1536, K3 3INST, bf16 x, T={T_head}",
             "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "K": K, "codebook": "3INST",
@@ -353,6 +383,7 @@ def main() -> int:
         },
         "per_batch": {
             f"T={T}": {"us_per_step": round(r["us_per_step"], 2), "GB/s": round(r["gbs"], 1),
+                       "eager_us_per_step": round(r["eager_us_per_step"], 2),
                        "distinct_experts": r["distinct_experts"],
                        "phase_us": {k: round(v, 2) for k, v in r["phase_us"].items()}}
             for T, r in results.items()

@@ -218,24 +218,139 @@ __device__ __forceinline__ void gateup_finish(const GemvParams& p, const Proj* g
     a1 = a[1] * kHadNorm;
 }
 
+// Position of input c of a row in the GEMV image: each 16 consecutive inputs
+// are stored in the MFMA k order of the GEMV (input c at pi_inv(c & 15)), so
+// a workgroup stages a row's tile rows with plain 16-byte copies.
+__device__ __forceinline__ int64_t image_pos(int64_t c) { return (c & ~15ll) + pi_inv((int)(c & 15)); }
+
+// Rotated activation rows for the decode GEMV, in image order:
+// img_q[row] = fp16(had128(fp16(x[token]) * suh_q) / sqrt(128)).  Linear:
+// row = token = the unit's row.  MoE: the unit's row is route r, the image row
+// is its sorted position route_pos[r] (dropped routes are skipped), token
+// r / topk, suh of the route's expert per projection.  One wave per (row,
+// 128-input block); computed once per row instead of once per workgroup.
+struct RotateArgs {
+    const void* x;
+    int x_dtype;
+    int64_t x_stride;
+    int in_f, n_rows;
+    const int* route_pos;   // null: linear
+    int topk;
+    const int* row_expert;
+    const uint16_t* suh;         // linear
+    const int64_t* suh_tab[2];   // MoE: per-expert suh of the two projections
+    int nproj;
+    uint16_t* img[2];
+};
+
+__global__ __launch_bounds__(256) void rotate_rows_kernel(RotateArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int nb = a.in_f >> 7;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= (int64_t)a.n_rows * nb) return;
+    const int r = (int)(unit / nb), hb = (int)(unit % nb);
+    int64_t row = r, tok = r;
+    int e = 0;
+    if (a.route_pos) {
+        const int pos = a.route_pos[r];
+        if (pos < 0) return;  // wave-uniform
+        row = pos;
+        tok = r / a.topk;
+        e = a.row_expert[pos];
+    }
+    const int64_t fb = (int64_t)hb * 128;
+    const float x0 = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane);
+    const float x1 = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane + 64);
+    for (int q = 0; q < a.nproj; ++q) {
+        const uint16_t* su =
+            a.route_pos ? reinterpret_cast<const uint16_t*>(a.suh_tab[q][e]) : a.suh;
+        float v0 = x0 * (float)bits_to_half(su[fb + lane]);
+        float v1 = x1 * (float)bits_to_half(su[fb + lane + 64]);
+        had128(v0, v1, lane);
+        uint16_t* dst = a.img[q] + row * a.in_f;
+        dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0 * kHadNorm));
+        dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1 * kHadNorm));
+    }
+}
+
+// Down-projection input rows, in image order: for every kept route, finish
+// gate/up (sum of the split partials, output rotation x svh, fp16 rounding,
+// activation, down suh, input rotation).  One wave per (route, 128-block of
+// the intermediate dimension); p carries the gate/up partials and tables.
+__global__ __launch_bounds__(256) void act_rows_kernel(GemvParams p, int n_routes, int topk,
+                                                       const int* route_pos, const int* row_expert,
+                                                       uint16_t* img) {
+    const int lane = threadIdx.x & 63;
+    const int inter = p.in_features;
+    const int nb = inter >> 7;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= (int64_t)n_routes * nb) return;
+    const int r = (int)(unit / nb), hb = (int)(unit % nb);
+    const int pos = route_pos[r];
+    if (pos < 0) return;  // wave-uniform
+    (void)topk;
+    const int e = row_expert[pos];
+    Proj gu[2];
+    gu[0].svh = reinterpret_cast<const uint16_t*>(p.tab[p.gateless ? 5 : 2][e]);
+    gu[1].svh = reinterpret_cast<const uint16_t*>(p.tab[5][e]);
+    const uint16_t* down_suh = reinterpret_cast<const uint16_t*>(p.tab[7][e]);
+    float a0, a1;
+    gateup_finish(p, gu, p.gateless ? 1 : 2, down_suh, pos, hb, lane, a0, a1);
+    uint16_t* dst = img + (int64_t)pos * inter;
+    dst[image_pos((int64_t)hb * 128 + lane)] = half_to_bits(f32_to_f16_rne(a0));
+    dst[image_pos((int64_t)hb * 128 + lane + 64)] = half_to_bits(f32_to_f16_rne(a1));
+}
+
 // Everything one projection of one row group needs, shared by all waves.
 struct RowGroup {
     int rg, nr, arow, row_base, hb_first, j, tiles_n, expert;
+    const void* img;  // rotated activation rows of the streamed projection
 };
 
-// Stage the rotated activations of one projection for chunk [c0, c0 + nb)
-// of 128-row blocks, stream its tiles, and add the result into red[row][128]
-// (waves in fixed order).  acc lives only inside this K-specialised routine.
-template <int K, int CB, int MODE>
+// Copy the rotated activations of a row group for tile rows [kt0, kt0 + nkt)
+// from their image (row-major fp16 rows, MFMA k order inside each 16 inputs)
+// into the LDS operand layout A[kt][MRB][16].  Every load of a batch is
+// issued before its stores, so the copy costs about one L2 round trip.
+__device__ __forceinline__ void stage_rows(const GemvParams& p, const RowGroup& G, int kt0, int nkt,
+                                           uint16_t* A, int tid) {
+    typedef __attribute__((address_space(1))) const v4u* gv4c;
+    const int MRB = p.MRB;
+    const int pieces = G.nr * nkt * 2;  // 16-byte pieces, row-major
+    const uint16_t* img = reinterpret_cast<const uint16_t*>(G.img);
+    constexpr int kBatch = 8;
+    for (int b0 = 0; b0 < pieces; b0 += kThreads * kBatch) {
+        v4u v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int pc = b0 + b * kThreads + tid;
+            if (pc < pieces) {
+                const int h = pc & 1, kt = (pc >> 1) % nkt, r = (pc >> 1) / nkt;
+                const int64_t row = G.row_base + G.rg + r;
+                v[b] = *(gv4c)(img + row * p.x_stride + (int64_t)(kt0 + kt) * 16 + 8 * h);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int pc = b0 + b * kThreads + tid;
+            if (pc < pieces) {
+                const int h = pc & 1, kt = (pc >> 1) % nkt, r = (pc >> 1) / nkt;
+                *reinterpret_cast<v4u*>(A + (kt * MRB + r) * 16 + 8 * h) = v[b];
+            }
+        }
+    }
+}
+
+// Stage the activations of one projection for chunk [c0, c0 + nb) of
+// 128-row blocks, stream its tiles, and leave each wave's partial sums in
+// red[wave][row][128].  acc lives only inside this K-specialised routine.
+template <int K, int CB>
 __device__ __forceinline__ void run_projection(const GemvParams& p, const RowGroup& G, const Proj& pq,
-                                               const Proj* gu, const uint16_t* down_suh,
                                                uint32_t* stage, uint16_t* A, float* red, int wave,
                                                int lane) {
     float4_t acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
     const int MRB = p.MRB;
-    const int gu_nproj = p.gateless ? 1 : 2;
     constexpr size_t tile_bytes = 32u * K;
     const size_t row_bytes = (size_t)G.tiles_n * tile_bytes;
     for (int c0 = 0; c0 < p.R_hb; c0 += p.C_hb) {
@@ -246,81 +361,30 @@ __device__ __forceinline__ void run_projection(const GemvParams& p, const RowGro
                             ((size_t)(G.hb_first + c0) * 8 * G.tiles_n + (size_t)G.j * 8) * tile_bytes;
         stream_prefetch<K>(rs, tb, row_bytes, nb * 8, wave, lane);
         __syncthreads();
-        const int units = G.nr * nb;
-        if constexpr (MODE == kModeDown) {
-            for (int u = wave; u < units; u += kWaves) {
-                const int r = u / nb, hb = u % nb;
-                float v0, v1;
-                gateup_finish(p, gu, gu_nproj, down_suh, G.row_base + G.rg + r, G.hb_first + c0 + hb,
-                              lane, v0, v1);
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int c = lane + 64 * h;
-                    A[((hb * 8 + (c >> 4)) * MRB + r) * 16 + pi_inv(c & 15)] =
-                        half_to_bits(f32_to_f16_rne(h ? v1 : v0));
-                }
-            }
-        } else {
-            // up to kUnitBatch units per wave: issue every load, then rotate
-            constexpr int kUnitBatch = 4;
-            for (int u0 = wave; u0 < units; u0 += kWaves * kUnitBatch) {
-                float xv[kUnitBatch][2], sv[kUnitBatch][2];
-#pragma unroll
-                for (int b = 0; b < kUnitBatch; ++b) {
-                    const int u = u0 + b * kWaves;
-                    if (u < units) {
-                        const int r = u / nb, hb = u % nb;
-                        const int64_t fb = (int64_t)(G.hb_first + c0 + hb) * 128;
-                        int64_t tok;
-                        if constexpr (MODE == kModeLinear)
-                            tok = G.rg + r;
-                        else
-                            tok = p.row_token[G.row_base + G.rg + r];
-                        xv[b][0] = load_act(p.x, p.x_dtype, tok * p.x_stride + fb + lane);
-                        xv[b][1] = load_act(p.x, p.x_dtype, tok * p.x_stride + fb + lane + 64);
-                        sv[b][0] = (float)bits_to_half(pq.suh[fb + lane]);
-                        sv[b][1] = (float)bits_to_half(pq.suh[fb + lane + 64]);
-                    }
-                }
-#pragma unroll
-                for (int b = 0; b < kUnitBatch; ++b) {
-                    const int u = u0 + b * kWaves;
-                    if (u < units) {
-                        const int r = u / nb, hb = u % nb;
-                        float v0 = xv[b][0] * sv[b][0], v1 = xv[b][1] * sv[b][1];
-                        had128(v0, v1, lane);
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            const int c = lane + 64 * h;
-                            A[((hb * 8 + (c >> 4)) * MRB + r) * 16 + pi_inv(c & 15)] =
-                                half_to_bits(f32_to_f16_rne((h ? v1 : v0) * kHadNorm));
-                        }
-                    }
-                }
-            }
-        }
+        stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
         __syncthreads();
         stream_consume<K, CB>(rs, wave, lane, stage, A, MRB, G.arow, acc);
     }
-    // cross-wave reduction, fixed wave order (every wave has finished reading
-    // A once it reaches the first barrier below)
+    // red overlays A: every wave must be done reading A first
+    __syncthreads();
     const int g = lane >> 4;
     const int col_nu = sigma_col(lane & 15);
-    for (int w = 0; w < kWaves; ++w) {
-        if (wave == w) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = 4 * g + i;
-                    if (row < G.nr) {
-                        float* dst = red + row * 128 + t * 16 + col_nu;
-                        *dst = (w == 0 ? 0.0f : *dst) + acc[t][i];
-                    }
-                }
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * g + i;
+            if (row < G.nr) red[(wave * MRB + row) * 128 + t * 16 + col_nu] = acc[t][i];
         }
-        __syncthreads();
-    }
+    __syncthreads();
+}
+
+// Sum of the four waves' partials at (row, column), in wave order.
+__device__ __forceinline__ float red_sum(const float* red, int MRB, int row, int c) {
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v += red[(w * MRB + row) * 128 + c];
+    return v;
 }
 
 template <int CB, int MODE>
@@ -349,14 +413,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         G.row_base = p.slot_start[slot];
         rows = p.slot_rows[slot];
     }
-    const int nproj = 1;  // projections streamed by this workgroup
-    Proj pr[2];
-    // Down: gate/up projections whose partials are finished while staging
-    Proj gu[2];
-    const uint16_t* down_suh = nullptr;
+    Proj pr;
     if constexpr (MODE == kModeLinear) {
-        pr[0] = {reinterpret_cast<const uint8_t*>(p.w_trellis), p.w_suh, p.w_svh, p.kuni[0]};
-        pr[1] = pr[0];
+        pr = {reinterpret_cast<const uint8_t*>(p.w_trellis), p.w_suh, p.w_svh, p.kuni[0]};
     } else {
         auto load_proj = [&](int pj) {
             Proj q;
@@ -366,44 +425,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
             q.K = p.ktab[pj] ? (int)p.ktab[pj][G.expert] : p.kuni[pj];
             return q;
         };
-        if constexpr (MODE == kModeGateUp) {
-            pr[0] = load_proj(p.gateless ? 1 : qsel);
-            pr[1] = pr[0];
-        } else {
-            pr[0] = load_proj(2);
-            pr[1] = pr[0];
-            gu[0] = load_proj(p.gateless ? 1 : 0);
-            gu[1] = load_proj(1);
-            down_suh = pr[0].suh;
-        }
+        pr = MODE == kModeGateUp ? load_proj(p.gateless ? 1 : qsel) : load_proj(2);
     }
 
     const int MRB = p.MRB;
+    G.img = (MODE == kModeGateUp && qsel) ? p.x2 : p.x;
     G.tiles_n = p.out_features >> 4;
     G.hb_first = s * p.R_hb;  // first 128-row input block of this split
-    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16][red: nproj x MRB x 128 fp32]
+    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16, later overlaid by
+    // red: 4 waves x MRB x 128 fp32]
     uint32_t* stage = reinterpret_cast<uint32_t*>(lds) + wave * (kStageBytes / 4);
     uint16_t* A = reinterpret_cast<uint16_t*>(lds + kWaves * kStageBytes);
-    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes + (size_t)p.C_hb * 8 * MRB * 32);
+    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes);
 
     for (G.rg = 0; G.rg < rows; G.rg += MRB) {
         G.nr = min(MRB, rows - G.rg);
         G.arow = min(lane & 15, G.nr - 1);
-        for (int q = 0; q < nproj; ++q) {
-            const Proj pq = q ? pr[1] : pr[0];
-            float* rq = red + q * MRB * 128;
-            switch (pq.K) {
-                case 2: run_projection<2, CB, MODE>(p, G, pq, gu, down_suh, stage, A, rq, wave, lane); break;
-                case 3: run_projection<3, CB, MODE>(p, G, pq, gu, down_suh, stage, A, rq, wave, lane); break;
-                case 4: run_projection<4, CB, MODE>(p, G, pq, gu, down_suh, stage, A, rq, wave, lane); break;
-                default: break;  // rejected on the host
-            }
+        switch (pr.K) {
+            case 2: run_projection<2, CB>(p, G, pr, stage, A, red, wave, lane); break;
+            case 3: run_projection<3, CB>(p, G, pr, stage, A, red, wave, lane); break;
+            case 4: run_projection<4, CB>(p, G, pr, stage, A, red, wave, lane); break;
+            default: break;  // rejected on the host
         }
         if (MODE == kModeLinear && p.S == 1) {
             // single split: finish in place
             for (int r = wave; r < G.nr; r += kWaves) {
-                float v0 = red[r * 128 + lane], v1 = red[r * 128 + lane + 64];
-                finish_block(v0, v1, pr[0].svh, G.j * 128 + lane, lane);
+                float v0 = red_sum(red, MRB, r, lane), v1 = red_sum(red, MRB, r, lane + 64);
+                finish_block(v0, v1, pr.svh, G.j * 128 + lane, lane);
                 const int64_t o = (int64_t)(G.rg + r) * p.out_stride + G.j * 128 + lane;
                 store_out(p.out, p.out_dtype, o, v0);
                 store_out(p.out, p.out_dtype, o + 64, v1);
@@ -412,7 +460,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
             for (int e = tid; e < G.nr * 128; e += kThreads) {
                 const int r = e >> 7, c = e & 127;
                 p.ws[(((int64_t)qsel * p.S + s) * p.n_rows_ws + G.row_base + G.rg + r) * p.out_features +
-                     G.j * 128 + c] = red[r * 128 + c];
+                     G.j * 128 + c] = red_sum(red, MRB, r, c);
             }
         }
         __syncthreads();
@@ -611,8 +659,9 @@ inline int pick_chunk(int R_hb, int nproj, int MRB) {
 
 inline size_t gemv_lds_bytes(int C_hb, int nproj, int MRB) {
     const size_t a = (size_t)C_hb * 8 * MRB * 16 * 2;
-    const size_t r = (size_t)nproj * MRB * 128 * 4;
-    return kWaves * kStageBytes + a + r;
+    (void)nproj;
+    const size_t r = (size_t)kWaves * MRB * 128 * 4;
+    return kWaves * kStageBytes + (a > r ? a : r);
 }
 
 struct PhasePlan {
@@ -633,7 +682,7 @@ inline PhasePlan plan_phase(int in_f, int base_items, int nproj, int MRB) {
 struct MoePlan {
     int n_routes, max_slots, MRB, nproj;
     PhasePlan gu, dn;
-    size_t off_route, off_wsgu, off_wsd, total;
+    size_t off_route, off_wsgu, off_wsd, off_img, off_imgd, total;
 };
 
 inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden, int64_t inter,
@@ -654,6 +703,10 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
     off += align256(4 * (size_t)m.nproj * m.gu.S * m.n_routes * inter);
     m.off_wsd = off;
     off += align256(4 * (size_t)m.dn.S * m.n_routes * hidden);
+    m.off_img = off;  // rotated gate/up input rows [nproj][routes][hidden] fp16
+    off += align256(2 * (size_t)m.nproj * m.n_routes * hidden);
+    m.off_imgd = off;  // down input rows [routes][inter] fp16
+    off += align256(2 * (size_t)m.n_routes * inter);
     m.total = off;
     return m;
 }
@@ -661,14 +714,16 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
 struct LinPlan {
     int MRB;
     PhasePlan ph;
-    size_t total;
+    size_t off_img, total;
 };
 
 inline LinPlan plan_linear(int64_t m, int64_t in_f, int64_t out_f) {
     LinPlan lp;
     lp.MRB = (int)(m < kMaxMRB ? m : kMaxMRB);
     lp.ph = plan_phase((int)in_f, (int)(out_f / 128), 1, lp.MRB);
-    lp.total = lp.ph.S > 1 ? align256(4 * (size_t)lp.ph.S * m * out_f) : 0;
+    // [split partials (S > 1)][rotated input rows, fp16]
+    lp.off_img = lp.ph.S > 1 ? align256(4 * (size_t)lp.ph.S * m * out_f) : 0;
+    lp.total = lp.off_img + align256(2 * (size_t)m * in_f);
     return lp;
 }
 
@@ -731,12 +786,22 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     EXL3_CHECK(x && trellis && suh && svh && out, "null pointer argument");
     const int64_t in_f = tiles_k * 16, out_f = tiles_n * 16;
     const LinPlan lp = plan_linear(m, in_f, out_f);
-    EXL3_CHECK(workspace_bytes >= (int64_t)lp.total && (lp.total == 0 || workspace),
+    EXL3_CHECK(workspace_bytes >= (int64_t)lp.total && workspace,
                "workspace too small: need %zu bytes", lp.total);
     EXL3_HIP(init_lds_caps());
+    uint16_t* img = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(workspace) + lp.off_img);
+    RotateArgs ra = {};
+    ra.x = x;
+    ra.x_dtype = x_dtype;
+    ra.x_stride = in_f;
+    ra.in_f = (int)in_f;
+    ra.n_rows = (int)m;
+    ra.suh = suh;
+    ra.nproj = 1;
+    ra.img[0] = img;
     GemvParams p = {};
-    p.x = x;
-    p.x_dtype = x_dtype;
+    p.x = img;
+    p.x_dtype = kF16;
     p.x_stride = in_f;
     p.w_trellis = trellis;
     p.w_suh = suh;
@@ -757,15 +822,19 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     profile_begin_call();
     profile_mark(0, st);
-    launch_gemv<kModeLinear>(codebook, (int)(out_f / 128) * lp.ph.S, lp.ph.lds, st, p);
+    const int64_t rot_units = m * (in_f / 128);
+    rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
     EXL3_LAUNCHED();
     profile_mark(1, st);
+    launch_gemv<kModeLinear>(codebook, (int)(out_f / 128) * lp.ph.S, lp.ph.lds, st, p);
+    EXL3_LAUNCHED();
+    profile_mark(2, st);
     if (lp.ph.S > 1) {
         const int items = (int)(m * (out_f / 128));
         linear_finish_kernel<<<(items + 3) / 4, 256, 0, st>>>(p.ws, lp.ph.S, (int)m, (int)out_f, svh,
                                                               out, out_dtype);
         EXL3_LAUNCHED();
-        profile_mark(2, st);
+        profile_mark(3, st);
     }
     return kOk;
 }
@@ -865,11 +934,34 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     p.act = act;
     float* ws_gu = reinterpret_cast<float*>(ws + mp.off_wsgu);
     float* ws_d = reinterpret_cast<float*>(ws + mp.off_wsd);
+    uint16_t* img_gu = reinterpret_cast<uint16_t*>(ws + mp.off_img);
+    uint16_t* img_d = reinterpret_cast<uint16_t*>(ws + mp.off_imgd);
+
+    // gate/up input rows, rotated once per route and projection
+    profile_mark(1, st);
+    RotateArgs ra = {};
+    ra.x = x;
+    ra.x_dtype = x_dtype;
+    ra.x_stride = hidden;
+    ra.in_f = (int)hidden;
+    ra.n_rows = mp.n_routes;
+    ra.route_pos = ro.route_pos;
+    ra.topk = (int)topk;
+    ra.row_expert = ro.row_expert;
+    ra.suh_tab[0] = tabs[1];
+    ra.suh_tab[1] = tabs[4];
+    ra.nproj = mp.nproj;
+    ra.img[0] = img_gu;
+    ra.img[1] = img_gu + (size_t)mp.n_routes * hidden;
+    const int64_t gu_units = (int64_t)mp.n_routes * (hidden / 128);
+    rotate_rows_kernel<<<(unsigned)((gu_units + 3) / 4), 256, 0, st>>>(ra);
+    EXL3_LAUNCHED();
 
     // gate/up: raw partial sums [nproj][S_gu][routes][inter]
     GemvParams pg = p;
-    pg.x = x;
-    pg.x_dtype = x_dtype;
+    pg.x = ra.img[0];
+    pg.x2 = ra.img[1];
+    pg.x_dtype = kF16;
     pg.x_stride = hidden;
     pg.in_features = (int)hidden;
     pg.out_features = (int)inter;
@@ -877,12 +969,12 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pg.R_hb = mp.gu.R_hb;
     pg.C_hb = mp.gu.C_hb;
     pg.ws = ws_gu;
-    profile_mark(1, st);
+    profile_mark(2, st);
     launch_gemv<kModeGateUp>(codebook, mp.max_slots * (int)(inter / 128) * mp.gu.S * mp.nproj,
                              mp.gu.lds, st, pg);
     EXL3_LAUNCHED();
 
-    // down: finishes gate/up while staging, raw partials [S_d][routes][hidden]
+    // down input rows: gate/up finished once per route
     GemvParams pd = p;
     pd.src_ws = ws_gu;
     pd.src_S = mp.gu.S;
@@ -892,15 +984,25 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pd.R_hb = mp.dn.R_hb;
     pd.C_hb = mp.dn.C_hb;
     pd.ws = ws_d;
-    profile_mark(2, st);
+    pd.x = img_d;
+    pd.x_dtype = kF16;
+    pd.x_stride = inter;
+    profile_mark(3, st);
+    const int64_t act_units = (int64_t)mp.n_routes * (inter / 128);
+    act_rows_kernel<<<(unsigned)((act_units + 3) / 4), 256, 0, st>>>(pd, mp.n_routes, (int)topk,
+                                                                     ro.route_pos, ro.row_expert, img_d);
+    EXL3_LAUNCHED();
+
+    // down: raw partials [S_d][routes][hidden]
+    profile_mark(4, st);
     launch_gemv<kModeDown>(codebook, mp.max_slots * (int)(hidden / 128) * mp.dn.S, mp.dn.lds, st, pd);
     EXL3_LAUNCHED();
 
-    profile_mark(3, st);
+    profile_mark(5, st);
     combine_kernel<<<(int)(T * (hidden / 128)), kCombineWaves * 64, 0, st>>>(
         ws_d, mp.dn.S, mp.n_routes, (int)hidden, ro.route_pos, ro.row_expert, down_svh, weights,
         w_dtype, (int)topk, out, out_dtype);
     EXL3_LAUNCHED();
-    profile_mark(4, st);
+    profile_mark(6, st);
     return kOk;
 }

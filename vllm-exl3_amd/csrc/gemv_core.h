@@ -41,9 +41,11 @@ constexpr int kDepth = 8;          // tile rows in flight per wave
 constexpr int kStageBytes = 1024;  // one tile row of 8 tiles at K <= 4
 
 struct GemvParams {
-    // Activations.  Linear / GateUp: raw rows [*, in] of x_dtype, gathered by
-    // row_token; Down: rotated fp16 rows [route_rows, in].
+    // Activations: rotated fp16 rows in the GEMV image order (see
+    // rotate_rows_kernel), [rows][x_stride]; linear rows are the input rows,
+    // MoE rows the sorted routes.  x2: the up projection's rows (gate/up).
     const void* x;
+    const void* x2;
     int x_dtype;
     int64_t x_stride;
     // Weights.  Linear: direct pointers.  MoE: device pointer tables indexed

@@ -16,7 +16,7 @@ import ctypes
 
 from . import _lib
 
-MOE_PHASES = ("route", "gate_up", "down", "combine")
+MOE_PHASES = ("route", "rotate", "gate_up", "act", "down", "combine")
 
 
 class PhaseTimer:
