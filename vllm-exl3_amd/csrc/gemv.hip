@@ -345,8 +345,8 @@ __device__ __forceinline__ void stage_rows(const GemvParams& p, const RowGroup& 
 // red[wave][row][128].  acc lives only inside this K-specialised routine.
 template <int K, int CB>
 __device__ __forceinline__ void run_projection(const GemvParams& p, const RowGroup& G, const Proj& pq,
-                                               uint32_t* stage, uint16_t* A, float* red, int wave,
-                                               int lane) {
+                                               uint32_t* stage, uint16_t* A, float* red, bool restage,
+                                               int wave, int lane) {
     float4_t acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -360,13 +360,15 @@ __device__ __forceinline__ void run_projection(const GemvParams& p, const RowGro
         const uint8_t* tb = pq.trellis +
                             ((size_t)(G.hb_first + c0) * 8 * G.tiles_n + (size_t)G.j * 8) * tile_bytes;
         stream_prefetch<K>(rs, tb, row_bytes, nb * 8, wave, lane);
-        __syncthreads();
-        stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
-        __syncthreads();
+        if (restage) {
+            __syncthreads();
+            stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
+            __syncthreads();
+        }
         stream_consume<K, CB>(rs, wave, lane, stage, A, MRB, G.arow, acc);
     }
-    // red overlays A: every wave must be done reading A first
-    __syncthreads();
+    // when red overlays A, every wave must be done reading A first
+    if (p.NJ == 1) __syncthreads();
     const int g = lane >> 4;
     const int col_nu = sigma_col(lane & 15);
 #pragma unroll
@@ -391,7 +393,7 @@ template <int CB, int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemv_kernel(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nJ = p.out_features >> 7;
+    const int nJB = (p.out_features >> 7) / p.NJ;  // blocks of NJ 128-column blocks
     // gate/up: each workgroup streams one of the two projections
     const int nsplit_proj = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
     const int item = blockIdx.x;
@@ -399,8 +401,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     const int s = (item / nsplit_proj) % p.S;
     const int rest = item / nsplit_proj / p.S;
     RowGroup G;
-    G.j = rest % nJ;
-    const int slot = rest / nJ;
+    const int jb = rest % nJB;
+    const int slot = rest / nJB;
 
     int rows;
     G.expert = 0;
@@ -432,19 +434,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     G.img = (MODE == kModeGateUp && qsel) ? p.x2 : p.x;
     G.tiles_n = p.out_features >> 4;
     G.hb_first = s * p.R_hb;  // first 128-row input block of this split
-    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16, later overlaid by
-    // red: 4 waves x MRB x 128 fp32]
+    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16][red: 4 waves x MRB x
+    // 128 fp32].  With one column block per workgroup red overlays A; with
+    // NJ > 1 (single-chunk phases only) A is staged once per row group and
+    // kept for every column block.
     uint32_t* stage = reinterpret_cast<uint32_t*>(lds) + wave * (kStageBytes / 4);
     uint16_t* A = reinterpret_cast<uint16_t*>(lds + kWaves * kStageBytes);
-    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes);
+    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes +
+                                          (p.NJ > 1 ? (size_t)p.C_hb * 8 * MRB * 32 : 0));
 
     for (G.rg = 0; G.rg < rows; G.rg += MRB) {
-        G.nr = min(MRB, rows - G.rg);
-        G.arow = min(lane & 15, G.nr - 1);
+      G.nr = min(MRB, rows - G.rg);
+      G.arow = min(lane & 15, G.nr - 1);
+      for (int jj = 0; jj < p.NJ; ++jj) {
+        G.j = jb * p.NJ + jj;
+        const bool restage = jj == 0;
         switch (pr.K) {
-            case 2: run_projection<2, CB>(p, G, pr, stage, A, red, wave, lane); break;
-            case 3: run_projection<3, CB>(p, G, pr, stage, A, red, wave, lane); break;
-            case 4: run_projection<4, CB>(p, G, pr, stage, A, red, wave, lane); break;
+            case 2: run_projection<2, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
+            case 3: run_projection<3, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
+            case 4: run_projection<4, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
             default: break;  // rejected on the host
         }
         if (MODE == kModeLinear && p.S == 1) {
@@ -464,6 +472,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
             }
         }
         __syncthreads();
+      }
     }
 }
 
@@ -635,17 +644,34 @@ __global__ __launch_bounds__(kCombineWaves * 64) void combine_kernel(
 // ---------------------------------------------------------------------------
 // Host-side planning (shared by the workspace queries and the launches)
 // ---------------------------------------------------------------------------
-constexpr int kTargetItems = 2048;
-constexpr int kMaxSplits = 4;
+constexpr int kMaxSplits = 16;
+// Column blocks per workgroup: the planner supports NJ > 1 (activations
+// staged once per row group), but on MI355X it measured slower than more,
+// shorter workgroups (each block's first rows wait on HBM again), so it is
+// capped at 1.
+constexpr int kMaxNJ = 1;
+// Launch cost model (microseconds, measured on MI355X under a full decode
+// load): a workgroup's fixed latency (argument, slot, table and activation
+// loads before its first tile row) and a wave's time per tile row with three
+// workgroups per CU (decode-VALU bound), plus the consumer's cost per split.
+constexpr double kWgFixedUs = 8.0;
+constexpr double kRowUs = 0.6;
+constexpr double kSplitUs = 0.15;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Largest divisor of n_hb with base_items * S <= target (at least 1).
-inline int pick_splits(int n_hb, int base_items) {
-    int best = 1;
-    for (int d = 1; d <= n_hb; ++d)
-        if (n_hb % d == 0 && d <= kMaxSplits && (int64_t)base_items * d <= kTargetItems) best = d;
-    return best;
+// Workgroups resident at once: three per CU (the GEMV's register budget).
+inline int resident_workgroups() {
+    static const int n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) {
+            (void)hipGetLastError();
+            cus = 256;
+        }
+        return 3 * cus;
+    }();
+    return n;
 }
 
 // Hadamard blocks whose activations fit the LDS budget at once.
@@ -657,26 +683,46 @@ inline int pick_chunk(int R_hb, int nproj, int MRB) {
     return c < R_hb ? c : R_hb;
 }
 
-inline size_t gemv_lds_bytes(int C_hb, int nproj, int MRB) {
+inline size_t gemv_lds_bytes(int C_hb, int NJ, int MRB) {
     const size_t a = (size_t)C_hb * 8 * MRB * 16 * 2;
-    (void)nproj;
     const size_t r = (size_t)kWaves * MRB * 128 * 4;
-    return kWaves * kStageBytes + (a > r ? a : r);
+    return kWaves * kStageBytes + (NJ > 1 ? a + r : (a > r ? a : r));
 }
 
 struct PhasePlan {
-    int S, R_hb, C_hb;
+    int S, R_hb, C_hb, NJ;
     size_t lds;
 };
 
-inline PhasePlan plan_phase(int in_f, int base_items, int nproj, int MRB) {
-    PhasePlan pp;
-    const int n_hb = in_f / 128;
-    pp.S = pick_splits(n_hb, base_items);
-    pp.R_hb = n_hb / pp.S;
-    pp.C_hb = pick_chunk(pp.R_hb, nproj, MRB);
-    pp.lds = gemv_lds_bytes(pp.C_hb, nproj, MRB);
-    return pp;
+// Split count S (a divisor of the input's 128-blocks) and column blocks per
+// workgroup NJ (a divisor of the output's 128-blocks; above 1 only when a
+// split's activations are staged in one chunk) minimising the modelled time:
+// rounds of resident workgroups x (fixed latency + NJ x rows per wave x row
+// time), plus the consumer's per-split cost.  base_items = slots x streamed
+// projections.
+inline PhasePlan plan_phase(int in_f, int out_f, int base_items, int MRB) {
+    const int n_hb = in_f / 128, n_j = out_f / 128;
+    const int cap = resident_workgroups();
+    PhasePlan best = {1, n_hb, pick_chunk(n_hb, 1, MRB), 1, 0};
+    double best_t = 1e30;
+    for (int S = 1; S <= kMaxSplits && S <= n_hb; ++S) {
+        if (n_hb % S) continue;
+        const int R_hb = n_hb / S;
+        const int C_hb = pick_chunk(R_hb, 1, MRB);
+        for (int NJ = 1; NJ <= kMaxNJ && NJ <= n_j; ++NJ) {
+            if (n_j % NJ || (NJ > 1 && C_hb < R_hb)) continue;
+            const int64_t items = (int64_t)base_items * (n_j / NJ) * S;
+            const int64_t rounds = (items + cap - 1) / cap;
+            const double rows = R_hb * 8.0 / kWaves;
+            const double t = rounds * (kWgFixedUs + NJ * rows * kRowUs) + S * kSplitUs;
+            if (t < best_t) {
+                best_t = t;
+                best = {S, R_hb, C_hb, NJ, 0};
+            }
+        }
+    }
+    best.lds = gemv_lds_bytes(best.C_hb, best.NJ, MRB);
+    return best;
 }
 
 struct MoePlan {
@@ -694,8 +740,8 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
     // slots run extra row groups (the weights are streamed once per group)
     m.MRB = (int)(T < kMoeMRB ? (T < 1 ? 1 : T) : kMoeMRB);
     m.nproj = gateless ? 1 : 2;
-    m.gu = plan_phase((int)hidden, m.max_slots * (int)(inter / 128) * m.nproj, 1, m.MRB);
-    m.dn = plan_phase((int)inter, m.max_slots * (int)(hidden / 128), 1, m.MRB);
+    m.gu = plan_phase((int)hidden, (int)inter, m.max_slots * m.nproj, m.MRB);
+    m.dn = plan_phase((int)inter, (int)hidden, m.max_slots, m.MRB);
     size_t off = 0;
     m.off_route = off;
     off += align256(sizeof(int) * (1 + 3 * (size_t)m.max_slots + 3 * (size_t)m.n_routes));
@@ -720,7 +766,7 @@ struct LinPlan {
 inline LinPlan plan_linear(int64_t m, int64_t in_f, int64_t out_f) {
     LinPlan lp;
     lp.MRB = (int)(m < kMaxMRB ? m : kMaxMRB);
-    lp.ph = plan_phase((int)in_f, (int)(out_f / 128), 1, lp.MRB);
+    lp.ph = plan_phase((int)in_f, (int)out_f, 1, lp.MRB);
     // [split partials (S > 1)][rotated input rows, fp16]
     lp.off_img = lp.ph.S > 1 ? align256(4 * (size_t)lp.ph.S * m * out_f) : 0;
     lp.total = lp.off_img + align256(2 * (size_t)m * in_f);
@@ -816,6 +862,7 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     p.S = lp.ph.S;
     p.R_hb = lp.ph.R_hb;
     p.C_hb = lp.ph.C_hb;
+    p.NJ = lp.ph.NJ;
     p.MRB = lp.MRB;
     p.n_rows_ws = (int)m;
     p.ws = reinterpret_cast<float*>(workspace);
@@ -826,7 +873,7 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
     EXL3_LAUNCHED();
     profile_mark(1, st);
-    launch_gemv<kModeLinear>(codebook, (int)(out_f / 128) * lp.ph.S, lp.ph.lds, st, p);
+    launch_gemv<kModeLinear>(codebook, (int)(out_f / 128 / lp.ph.NJ) * lp.ph.S, lp.ph.lds, st, p);
     EXL3_LAUNCHED();
     profile_mark(2, st);
     if (lp.ph.S > 1) {
@@ -968,9 +1015,10 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pg.S = mp.gu.S;
     pg.R_hb = mp.gu.R_hb;
     pg.C_hb = mp.gu.C_hb;
+    pg.NJ = mp.gu.NJ;
     pg.ws = ws_gu;
     profile_mark(2, st);
-    launch_gemv<kModeGateUp>(codebook, mp.max_slots * (int)(inter / 128) * mp.gu.S * mp.nproj,
+    launch_gemv<kModeGateUp>(codebook, mp.max_slots * (int)(inter / 128 / mp.gu.NJ) * mp.gu.S * mp.nproj,
                              mp.gu.lds, st, pg);
     EXL3_LAUNCHED();
 
@@ -983,6 +1031,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pd.S = mp.dn.S;
     pd.R_hb = mp.dn.R_hb;
     pd.C_hb = mp.dn.C_hb;
+    pd.NJ = mp.dn.NJ;
     pd.ws = ws_d;
     pd.x = img_d;
     pd.x_dtype = kF16;
@@ -995,7 +1044,8 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
 
     // down: raw partials [S_d][routes][hidden]
     profile_mark(4, st);
-    launch_gemv<kModeDown>(codebook, mp.max_slots * (int)(hidden / 128) * mp.dn.S, mp.dn.lds, st, pd);
+    launch_gemv<kModeDown>(codebook, mp.max_slots * (int)(hidden / 128 / mp.dn.NJ) * mp.dn.S, mp.dn.lds, st,
+                           pd);
     EXL3_LAUNCHED();
 
     profile_mark(5, st);

@@ -9,7 +9,7 @@
 //     slot (no workgroup barrier in the main loop);
 //   * each lane reads the two uint32 words that cover the windows of its four
 //     consecutive tile indices, funnel-shifts them once, and decodes four
-//     weights with bfe / mad_u32_u24 / pk_mad_u16 / bitop3;
+//     weights with bfe / one full-rate 32-bit multiply / bitop3 each;
 //   * the codebook's (lo, hi) half pair is fed to MFMA as-is: the K dimension
 //     is doubled (each activation duplicated), so the hardware sums the two
 //     halves in fp32 and no fp16 add, pack or permute is spent per weight;
@@ -20,10 +20,10 @@
 // the matching permuted, duplicated order, and results are un-permuted when
 // they leave the accumulators.
 //
-// Split-K partials go to a workspace; the last workgroup of a column block
-// (an agent-scope counter that the finisher resets) sums them in split order
-// and runs the epilogue: output 128-Hadamard x svh, and for the MoE gate/up
-// phase the SwiGLU plus the down projection's input rotation.
+// Split-K partials go to a workspace and the consumer kernel sums them in
+// split order and runs the epilogue: output 128-Hadamard x svh, and after the
+// MoE gate/up phase the activation plus the down projection's input rotation.
+// Activations arrive pre-rotated (one rotation per row, not per workgroup).
 #pragma once
 
 #include "exl3_common.h"
@@ -79,6 +79,7 @@ struct GemvParams {
     int S;         // splits of the input dimension
     int R_hb;      // 128-row Hadamard blocks per split
     int C_hb;      // Hadamard blocks whose activations are staged at once
+    int NJ;        // 128-column blocks per workgroup (activations staged once)
     int MRB;       // rows per row group (<= 16)
     int n_rows_ws; // rows addressed in the workspace (route rows or m)
     float* ws;
@@ -134,36 +135,42 @@ __device__ __forceinline__ LaneWords lane_words(int lane) {
 
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
+// The codebook hash x = w*C (+ add for 3INST) mod 2^32 of one 16-bit window
+// w (clean: bits above 15 zero).  On gfx950 the 32-bit multiply
+// (v_mul_lo_u32) and the 64-bit multiply-add (v_mad_u64_u32, low half kept)
+// issue at the full VALU rate, so the whole 32-bit product is one op.
+// (The compiler splits a 64-bit multiply-add whose high half is unused into
+// a multiply and an add, so the 3INST form is written as the instruction:
+// the multiplier in an SGPR, the addend in a VGPR pair - one constant-bus
+// read - and its result only feeds ordinary VALU ops.)
+template <int CB>
+__device__ __forceinline__ uint32_t hash32(uint32_t w) {
+    if constexpr (CB == kCb3Inst) {
+        uint64_t r, carry;
+        asm("v_mad_u64_u32 %0, %1, %2, %3, %4"
+            : "=v"(r), "=s"(carry)
+            : "v"(w), "s"(89226354u), "v"((uint64_t)64248484u));
+        return (uint32_t)r;
+    } else {
+        return w * 0xCBAC1FEDu;
+    }
+}
+
 // Decode the lane's four weights of one tile into MFMA B registers (each a
 // (lo, hi) fp16 pair whose sum is the weight).  Per weight, for the two
-// "sum of halves" codebooks: one shift (none for the last window), then
-// x*C mod 2^32 = x*C_lo + ((x*C_hi) << 16) as v_mad_u32_u16 (the 16-bit
-// multiplier reads only the window's low 16 bits, so no mask is needed; the
-// 3INST addend folds in) plus one v_pk_mad_u16 whose low lane adds 0, and one
-// v_bitop3 for the mask/xor: four VALU ops per weight.
+// "sum of halves" codebooks: one bit-field extract of the window, one
+// full-rate multiply for the hash and one v_bitop3 for the mask/xor: three
+// VALU ops per weight (plus one funnel shift per four weights).
 template <int K, int CB>
 __device__ __forceinline__ void decode4(uint32_t hi, uint32_t lo, uint32_t shift, uint32_t b[4]) {
     const uint32_t s = __builtin_amdgcn_alignbit(hi, lo, shift);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t sh = s >> ((3 - i) * K);
+        const uint32_t w = (s >> ((3 - i) * K)) & 0xFFFFu;
         if constexpr (CB == kCbMul1) {
-            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(sh & 0xFFFFu));  // (value, +0)
+            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(w));  // (value, +0)
         } else {
-            constexpr uint32_t C = (CB == kCb3Inst) ? 89226354u : 0xCBAC1FEDu;
-            const uint32_t c_lo = C & 0xFFFFu;
-            uint32_t lo_prod;
-            if constexpr (CB == kCb3Inst) {
-                const uint32_t add = 64248484u;
-                asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(lo_prod) : "v"(sh), "s"(c_lo), "v"(add));
-            } else {
-                asm("v_mad_u32_u16 %0, %1, %2, 0" : "=v"(lo_prod) : "v"(sh), "s"(c_lo));
-            }
-            const unsigned short w16 = (unsigned short)sh;
-            const u16x2_t xv = {w16, w16};
-            const u16x2_t cv = {(unsigned short)0, (unsigned short)(C >> 16)};
-            const u16x2_t r = xv * cv + __builtin_bit_cast(u16x2_t, lo_prod);
-            b[i] = (__builtin_bit_cast(uint32_t, r) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+            b[i] = (hash32<CB>(w) & 0x8FFF8FFFu) ^ 0x3B603B60u;
         }
     }
 }
