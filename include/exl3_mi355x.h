@@ -74,6 +74,23 @@ int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* trellis, int
               void* out, int out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Batched decode GEMV: one linear per listed expert over the same input rows,
+ * out[i] = exl3_gemm(x, W[expert_indices[i]]) as [n_sel, m, out_features]
+ * of out_dtype.  Tables are int64 device arrays of device addresses with
+ * n_ptr entries; expert_indices is a device int32 [n_sel]; an index outside
+ * [0, n_ptr) yields zero rows.  K in {2,3,4}, any codebook, any m >= 1.
+ * Replaces vllm_exl3_c.p2b_gemv_batched (csrc/bindings.cpp:149-156,
+ * csrc/p2b_batched.cu:341-368; the reference fixes out_features at 2048 and
+ * the codebook at MCG). */
+int64_t exl3_gemv_batched_workspace_size(int64_t m, int64_t n_sel, int64_t in_features,
+                                         int64_t out_features);
+int exl3_gemv_batched(const void* x, int x_dtype, int64_t m, int64_t in_features,
+                      int64_t out_features, const int64_t* trellis_tab, const int64_t* suh_tab,
+                      const int64_t* svh_tab, int64_t n_ptr, const int32_t* expert_indices,
+                      int64_t n_sel, int64_t K, int codebook, void* out, int out_dtype,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Routed-expert MoE forward for T decode rows in one launch sequence:
  * device-side routing sort -> fused gate/up GEMV + activation + down-input
  * rotation -> down GEMV -> per-token combine in slot order (no atomics in

@@ -70,3 +70,56 @@ def test_gemm_deterministic(gpu):
     a = _run(lin, x, 1, gpu, torch.float32)
     b = _run(lin, x, 1, gpu, torch.float32)
     assert torch.equal(a, b)
+
+
+def _batched_layer(gpu, seed, n, in_f, out_f, K):
+    packs = [S.linear(seed + e, in_f, out_f, K) for e in range(n)]
+    dev = [{k: torch.from_numpy(p[k]).to(gpu) for k in ("trellis", "suh", "svh")} for p in packs]
+    tabs = [torch.tensor([d[k].data_ptr() for d in dev], dtype=torch.int64, device=gpu)
+            for k in ("trellis", "suh", "svh")]
+    return packs, dev, tabs
+
+
+@pytest.mark.parametrize("K,cb,m", [(2, 1, 1), (3, 0, 5), (4, 2, 3)])
+def test_gemv_batched_vs_oracle_and_sequential(gpu, K, cb, m):
+    # p2b_gemv_batched: entry i == exl3_gemv(x, W[idx_i]); repeated ids, and an
+    # id outside the tables gives zeros (csrc/p2b_batched.cu:341-368)
+    packs, dev, tabs = _batched_layer(gpu, 4000 + 10 * K + cb, 4, 512, 256, K)
+    x = S.activations(40 + m, m, 512)
+    xt = torch.from_numpy(x).to(gpu).half()
+    idx = torch.tensor([3, 0, 3, 9, 1], dtype=torch.int32, device=gpu)
+    got = C.p2b_gemv_batched(xt, *tabs, idx, K, cb == 1, codebook=cb, out_features=256)
+    assert got.shape == (5, m, 256) and got.dtype == torch.float16
+    assert torch.count_nonzero(got[3]) == 0
+    for i, e in enumerate([3, 0, 3, None, 1]):
+        if e is None:
+            continue
+        w = O.dequant(packs[e]["trellis"], packs[e]["suh"], packs[e]["svh"], K, cb)
+        assert rel_l2(got[i], O.gemv(xt.float().cpu().numpy(), w)) <= TOL
+        seq = C.exl3_gemm(xt, dev[e]["trellis"], dev[e]["suh"], dev[e]["svh"], K, cb == 1, codebook=cb)
+        assert (got[i].float() - seq.float()).abs().max().item() <= 1e-3
+
+
+def test_gemv_batched_reference_shape_and_split_path(gpu):
+    # the reference's test shape: 8 experts, K2 MCG, 4096 -> 2048, m = 1
+    # (long input dimension: the split-K finisher path)
+    packs, dev, tabs = _batched_layer(gpu, 5000, 8, 4096, 2048, 2)
+    x = S.activations(50, 1, 4096)
+    xt = torch.from_numpy(x).to(gpu).half()
+    idx = torch.arange(8, dtype=torch.int64, device=gpu)
+    got = C.p2b_gemv_batched(xt, *tabs, idx, 2, True)
+    assert got.shape == (8, 1, 2048)
+    for e in (0, 5, 7):
+        w = O.dequant(packs[e]["trellis"], packs[e]["suh"], packs[e]["svh"], 2, 1)
+        assert rel_l2(got[e], O.gemv(x, w)) <= TOL
+    # graph replay with new activations matches eager launches
+    out = torch.empty_like(got)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out.copy_(C.p2b_gemv_batched(xt, *tabs, idx, 2, True))
+    for seed in (51, 52):
+        xt.copy_(torch.from_numpy(S.activations(seed, 1, 4096)))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, C.p2b_gemv_batched(xt, *tabs, idx, 2, True))

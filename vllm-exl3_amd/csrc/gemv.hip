@@ -241,6 +241,10 @@ struct RotateArgs {
     const int64_t* suh_tab[2];   // MoE: per-expert suh of the two projections
     int nproj;
     uint16_t* img[2];
+    // batched: row r = (slot r / batch_m, input row r % batch_m), suh of the
+    // slot's expert from suh_tab[0]; rows of ids outside the table are skipped
+    const int* expert_list;
+    int batch_m, n_ptr;
 };
 
 __global__ __launch_bounds__(256) void rotate_rows_kernel(RotateArgs a) {
@@ -257,13 +261,18 @@ __global__ __launch_bounds__(256) void rotate_rows_kernel(RotateArgs a) {
         row = pos;
         tok = r / a.topk;
         e = a.row_expert[pos];
+    } else if (a.expert_list) {
+        e = a.expert_list[r / a.batch_m];
+        if (e < 0 || e >= a.n_ptr) return;  // wave-uniform
+        tok = r % a.batch_m;
     }
     const int64_t fb = (int64_t)hb * 128;
     const float x0 = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane);
     const float x1 = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane + 64);
     for (int q = 0; q < a.nproj; ++q) {
-        const uint16_t* su =
-            a.route_pos ? reinterpret_cast<const uint16_t*>(a.suh_tab[q][e]) : a.suh;
+        const uint16_t* su = (a.route_pos || a.expert_list)
+                                 ? reinterpret_cast<const uint16_t*>(a.suh_tab[q][e])
+                                 : a.suh;
         float v0 = x0 * (float)bits_to_half(su[fb + lane]);
         float v1 = x1 * (float)bits_to_half(su[fb + lane + 64]);
         had128(v0, v1, lane);
@@ -409,6 +418,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     if constexpr (MODE == kModeLinear) {
         rows = p.m_rows;
         G.row_base = 0;
+    } else if constexpr (MODE == kModeBatched) {
+        if (slot >= p.max_slots) return;
+        G.expert = p.expert_list[slot];
+        G.row_base = slot * p.batch_m;
+        rows = p.batch_m;
+        if (G.expert < 0 || G.expert >= p.n_ptr) {
+            // not a table entry: zero outputs (written by the finisher when split)
+            if (p.S == 1)
+                for (int e = tid; e < rows * 128 * p.NJ; e += kThreads)
+                    store_out(p.out, p.out_dtype,
+                              (int64_t)(G.row_base + (e >> 7) % rows) * p.out_stride +
+                                  (jb * p.NJ + (e >> 7) / rows) * 128 + (e & 127),
+                              0.0f);
+            return;
+        }
     } else {
         if (slot >= *p.n_active) return;
         G.expert = p.slot_expert[slot];
@@ -418,6 +442,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     Proj pr;
     if constexpr (MODE == kModeLinear) {
         pr = {reinterpret_cast<const uint8_t*>(p.w_trellis), p.w_suh, p.w_svh, p.kuni[0]};
+    } else if constexpr (MODE == kModeBatched) {
+        pr = {reinterpret_cast<const uint8_t*>(p.tab[0][G.expert]),
+              reinterpret_cast<const uint16_t*>(p.tab[1][G.expert]),
+              reinterpret_cast<const uint16_t*>(p.tab[2][G.expert]), p.kuni[0]};
     } else {
         auto load_proj = [&](int pj) {
             Proj q;
@@ -455,12 +483,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
             case 4: run_projection<4, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
             default: break;  // rejected on the host
         }
-        if (MODE == kModeLinear && p.S == 1) {
+        if ((MODE == kModeLinear || MODE == kModeBatched) && p.S == 1) {
             // single split: finish in place
             for (int r = wave; r < G.nr; r += kWaves) {
                 float v0 = red_sum(red, MRB, r, lane), v1 = red_sum(red, MRB, r, lane + 64);
                 finish_block(v0, v1, pr.svh, G.j * 128 + lane, lane);
-                const int64_t o = (int64_t)(G.rg + r) * p.out_stride + G.j * 128 + lane;
+                const int64_t o = (int64_t)(G.row_base + G.rg + r) * p.out_stride + G.j * 128 + lane;
                 store_out(p.out, p.out_dtype, o, v0);
                 store_out(p.out, p.out_dtype, o + 64, v1);
             }
@@ -477,19 +505,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 }
 
 // Linear with split-K: out[m] = finish(sum of splits).  One wave per
-// (row, 128-column block).
+// (row, 128-column block).  Batched: row r belongs to slot r / batch_m, whose
+// expert's svh comes from svh_tab (ids outside the table give zeros).
+struct FinishBatch {
+    const int64_t* svh_tab;  // null: single linear
+    const int* expert_list;
+    int batch_m, n_ptr;
+};
+
 __global__ __launch_bounds__(256) void linear_finish_kernel(const float* __restrict__ ws, int S,
                                                             int m, int out_f,
                                                             const uint16_t* __restrict__ svh,
-                                                            void* out, int out_dtype) {
+                                                            void* out, int out_dtype, FinishBatch fb) {
     const int lane = threadIdx.x & 63;
     const int nJ = out_f >> 7;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= m * nJ) return;
     const int r = item / nJ, j = item % nJ;
     float v0 = 0.f, v1 = 0.f;
-    sum_splits(ws + (int64_t)r * out_f, (int64_t)m * out_f, S, j * 128 + lane, v0, v1);
-    finish_block(v0, v1, svh, j * 128 + lane, lane);
+    bool zero = false;
+    if (fb.svh_tab) {
+        const int e = fb.expert_list[r / fb.batch_m];
+        zero = e < 0 || e >= fb.n_ptr;  // wave-uniform
+        if (!zero) svh = reinterpret_cast<const uint16_t*>(fb.svh_tab[e]);
+    }
+    if (!zero) {
+        sum_splits(ws + (int64_t)r * out_f, (int64_t)m * out_f, S, j * 128 + lane, v0, v1);
+        finish_block(v0, v1, svh, j * 128 + lane, lane);
+    }
     const int64_t o = (int64_t)r * out_f + j * 128 + lane;
     store_out(out, out_dtype, o, v0);
     store_out(out, out_dtype, o + 64, v1);
@@ -786,8 +829,9 @@ hipError_t init_lds_caps() {
     static const hipError_t st = [] {
         hipError_t e = hipSuccess;
         hipError_t r[] = {set_lds_cap<0, 0>(), set_lds_cap<0, 1>(), set_lds_cap<0, 2>(),
-                          set_lds_cap<1, 0>(), set_lds_cap<1, 1>(), set_lds_cap<1, 2>(),
-                          set_lds_cap<2, 0>(), set_lds_cap<2, 1>(), set_lds_cap<2, 2>()};
+                          set_lds_cap<0, 3>(), set_lds_cap<1, 0>(), set_lds_cap<1, 1>(),
+                          set_lds_cap<1, 2>(), set_lds_cap<1, 3>(), set_lds_cap<2, 0>(),
+                          set_lds_cap<2, 1>(), set_lds_cap<2, 2>(), set_lds_cap<2, 3>()};
         for (hipError_t x : r)
             if (x != hipSuccess) e = x;
         return e;
@@ -879,9 +923,108 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     if (lp.ph.S > 1) {
         const int items = (int)(m * (out_f / 128));
         linear_finish_kernel<<<(items + 3) / 4, 256, 0, st>>>(p.ws, lp.ph.S, (int)m, (int)out_f, svh,
-                                                              out, out_dtype);
+                                                              out, out_dtype, FinishBatch{});
         EXL3_LAUNCHED();
         profile_mark(3, st);
+    }
+    return kOk;
+}
+
+struct BatchPlan {
+    int MRB;
+    PhasePlan ph;
+    size_t off_img, total;
+};
+
+inline BatchPlan plan_batched(int64_t m, int64_t n_sel, int64_t in_f, int64_t out_f) {
+    BatchPlan bp;
+    bp.MRB = (int)(m < kMaxMRB ? m : kMaxMRB);
+    bp.ph = plan_phase((int)in_f, (int)out_f, (int)n_sel, bp.MRB);
+    // [split partials (S > 1)][rotated input rows per slot, fp16]
+    bp.off_img = bp.ph.S > 1 ? align256(4 * (size_t)bp.ph.S * n_sel * m * out_f) : 0;
+    bp.total = bp.off_img + align256(2 * (size_t)n_sel * m * in_f);
+    return bp;
+}
+
+EXL3_API int64_t exl3_gemv_batched_workspace_size(int64_t m, int64_t n_sel, int64_t in_features,
+                                                  int64_t out_features) {
+    if (m < 1 || n_sel < 1 || in_features < 128 || out_features < 128) return 0;
+    return (int64_t)plan_batched(m, n_sel, in_features, out_features).total;
+}
+
+EXL3_API int exl3_gemv_batched(const void* x, int x_dtype, int64_t m, int64_t in_features,
+                               int64_t out_features, const int64_t* trellis_tab,
+                               const int64_t* suh_tab, const int64_t* svh_tab, int64_t n_ptr,
+                               const int32_t* expert_indices, int64_t n_sel, int64_t K, int codebook,
+                               void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+    EXL3_CHECK(K == 2 || K == 3 || K == 4, "batched GEMV supports K=2,3,4");
+    EXL3_CHECK(codebook >= 0 && codebook <= 2, "codebook must be 0 (3INST), 1 (MCG) or 2 (mul1)");
+    EXL3_CHECK(x_dtype >= 0 && x_dtype <= 2 && out_dtype >= 0 && out_dtype <= 2,
+               "dtype ids: 0 fp16, 1 bf16, 2 fp32");
+    EXL3_CHECK(m >= 1 && n_sel >= 1 && n_ptr >= 1 && n_sel * m <= (1 << 24),
+               "batched GEMV needs m >= 1, at least one expert index and one table entry");
+    EXL3_CHECK(in_features % 128 == 0 && out_features % 128 == 0 && in_features > 0 && out_features > 0 &&
+                   in_features <= (1 << 20) && out_features <= (1 << 20),
+               "batched GEMV feature dimensions must be positive multiples of 128");
+    EXL3_CHECK(in_features * out_features / 16 * K / 8 * 16 < (1ll << 31),
+               "packed trellis must be smaller than 2 GiB");
+    EXL3_CHECK(x && trellis_tab && suh_tab && svh_tab && expert_indices && out,
+               "null pointer argument");
+    const BatchPlan bp = plan_batched(m, n_sel, in_features, out_features);
+    EXL3_CHECK(workspace && workspace_bytes >= (int64_t)bp.total,
+               "workspace too small: need %zu bytes", bp.total);
+    EXL3_HIP(init_lds_caps());
+    uint16_t* img = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(workspace) + bp.off_img);
+    RotateArgs ra = {};
+    ra.x = x;
+    ra.x_dtype = x_dtype;
+    ra.x_stride = in_features;
+    ra.in_f = (int)in_features;
+    ra.n_rows = (int)(n_sel * m);
+    ra.suh_tab[0] = suh_tab;
+    ra.nproj = 1;
+    ra.img[0] = img;
+    ra.expert_list = expert_indices;
+    ra.batch_m = (int)m;
+    ra.n_ptr = (int)n_ptr;
+    GemvParams p = {};
+    p.x = img;
+    p.x_dtype = kF16;
+    p.x_stride = in_features;
+    p.tab[0] = trellis_tab;
+    p.tab[1] = suh_tab;
+    p.tab[2] = svh_tab;
+    p.kuni[0] = (int)K;
+    p.in_features = (int)in_features;
+    p.out_features = (int)out_features;
+    p.max_slots = (int)n_sel;
+    p.expert_list = expert_indices;
+    p.n_ptr = (int)n_ptr;
+    p.batch_m = (int)m;
+    p.out = out;
+    p.out_dtype = out_dtype;
+    p.out_stride = out_features;
+    p.S = bp.ph.S;
+    p.R_hb = bp.ph.R_hb;
+    p.C_hb = bp.ph.C_hb;
+    p.NJ = bp.ph.NJ;
+    p.MRB = bp.MRB;
+    p.n_rows_ws = (int)(n_sel * m);
+    p.ws = reinterpret_cast<float*>(workspace);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int64_t rot_units = n_sel * m * (in_features / 128);
+    rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
+    EXL3_LAUNCHED();
+    launch_gemv<kModeBatched>(codebook, (int)(n_sel * (out_features / 128 / bp.ph.NJ) * bp.ph.S),
+                              bp.ph.lds, st, p);
+    EXL3_LAUNCHED();
+    if (bp.ph.S > 1) {
+        const int64_t items = n_sel * m * (out_features / 128);
+        FinishBatch fb{svh_tab, expert_indices, (int)m, (int)n_ptr};
+        linear_finish_kernel<<<(unsigned)((items + 3) / 4), 256, 0, st>>>(
+            p.ws, bp.ph.S, (int)(n_sel * m), (int)out_features, nullptr, out, out_dtype, fb);
+        EXL3_LAUNCHED();
     }
     return kOk;
 }

@@ -30,7 +30,7 @@
 
 namespace exl3 {
 
-enum GemvMode : int { kModeLinear = 0, kModeGateUp = 1, kModeDown = 2 };
+enum GemvMode : int { kModeLinear = 0, kModeGateUp = 1, kModeDown = 2, kModeBatched = 3 };
 // Activation ids follow the reference (src/vllm_exl3/exl3.py MOE_ACT_*):
 enum ActId : int { kActSilu = 0, kActRelu2 = 2, kActSwigluOai = 3 };
 enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
@@ -66,6 +66,12 @@ struct GemvParams {
     const int* row_token;
     int max_slots;
     int m_rows;  // linear: number of rows
+    // Batched (one linear per listed expert, same input rows): the expert of
+    // each slot, the table size (ids outside [0, n_ptr) give zero outputs)
+    // and the rows per slot.
+    const int* expert_list;
+    int n_ptr;
+    int batch_m;
     // Output.  Linear: out_dtype rows [m, out]; GateUp: fp16 act_h rows
     // [route_rows, inter] (already rotated for the down projection); Down:
     // fp32 rows [route_rows, hidden].

@@ -28,6 +28,9 @@ SIGNATURES: dict[str, list] = {
     "exl3_decode_tiles": [_p, _i64, _i64, _i64, _i32, _p, _p],
     "exl3_gemm_workspace_size": [_i64, _i64, _i64],
     "exl3_gemm": [_p, _i32, _i64, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i32, _p, _i64, _p],
+    "exl3_gemv_batched_workspace_size": [_i64, _i64, _i64, _i64],
+    "exl3_gemv_batched": [_p, _i32, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i32, _p, _i32,
+                          _p, _i64, _p],
     "exl3_moe_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i32],
     "exl3_moe_forward": [_p, _i32, _i64, _i64, _i64] + [_p] * 9 + [_i64, _p, _p, _p, _i64, _i64, _i64,
                          _i32, _i32, _i32, _f32, _p, _i32, _p, _i32, _i64, _p, _p, _i32, _p, _i64, _p],
@@ -50,6 +53,7 @@ SIGNATURES: dict[str, list] = {
 }
 _RESTYPES = {"exl3_last_error": ctypes.c_char_p, "exl3_gemm_workspace_size": _i64,
              "exl3_moe_workspace_size": _i64, "exl3_fat_gemm_workspace_size": _i64,
+             "exl3_gemv_batched_workspace_size": _i64,
              "exl3_moe_prefill_workspace_size": _i64, "exl3_kv_page_bytes": _i64,
              "exl3_kv_decode_workspace_size": _i64}
 

@@ -199,6 +199,53 @@ def exl3_gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: to
     return out if x.is_cuda else out.to(x.device)
 
 
+def p2b_gemv_batched(x: torch.Tensor, trellis_ptrs: torch.Tensor, suh_ptrs: torch.Tensor,
+                     svh_ptrs: torch.Tensor, expert_indices: torch.Tensor, K: int, mcg: bool,
+                     mmode: int = 1, *, out_features: int = 2048, mul1: bool = False,
+                     codebook: int | None = None) -> torch.Tensor:
+    """One EXL3 linear per listed expert over the same rows: fp16
+    [len(expert_indices), m, out_features], entry i equal to
+    ``exl3_gemv(x, trellis[e_i], suh[e_i], svh[e_i], K, mcg)``.
+    csrc/bindings.cpp:149-156, csrc/p2b_batched.cu:341-368.
+
+    Same arguments as the reference (which fixes out_features at 2048 and the
+    codebook at MCG); ``out_features`` and ``mul1``/``codebook`` are keyword
+    extensions.  Pointer tables are int64 device tensors of device addresses
+    owned by the caller; an index outside the tables yields zero rows.  One
+    launch sequence on the current stream, no host synchronisation."""
+    _check(mmode in (0, 1), "mmode must be 0 or 1")
+    K = int(K)
+    _check(K in (2, 3, 4), "batched GEMV supports K=2,3,4")
+    _check(x.dim() >= 2 and x.numel() > 0, "x must have shape [..., in_features]")
+    dev = _gpu_device(x)
+    for t, nm in ((trellis_ptrs, "trellis_ptrs"), (suh_ptrs, "suh_ptrs"), (svh_ptrs, "svh_ptrs")):
+        _check(t.dtype == torch.int64 and t.dim() == 1 and t.is_cuda and t.device == dev,
+               f"{nm} must be an int64 device vector on x's device")
+    _check(trellis_ptrs.numel() == suh_ptrs.numel() == svh_ptrs.numel() and trellis_ptrs.numel() > 0,
+           "pointer tables must have the same, non-zero length")
+    _check(expert_indices.dtype in (torch.int32, torch.int64) and expert_indices.is_cuda
+           and expert_indices.device == dev and expert_indices.numel() > 0,
+           "expert_indices must be a non-empty int32/int64 device tensor on x's device")
+    in_f = x.size(-1)
+    _check(in_f % 128 == 0 and int(out_features) % 128 == 0,
+           "batched GEMV feature dimensions must be multiples of 128")
+    cb = codebook_id(mcg, mul1, codebook)
+    m = x.numel() // in_f
+    e = expert_indices.numel()
+    x2 = x.contiguous().view(m, in_f)
+    idx = expert_indices.reshape(-1).to(torch.int32).contiguous()
+    tp, sp, vp = (t.contiguous() for t in (trellis_ptrs, suh_ptrs, svh_ptrs))
+    out = torch.empty((e, m, int(out_features)), dtype=torch.float16, device=dev)
+    lib = _lib.load()
+    need = int(lib.exl3_gemv_batched_workspace_size(m, e, in_f, int(out_features)))
+    ws = workspace(dev, "gemv_batched", need)
+    with torch.cuda.device(dev):
+        _lib.call("exl3_gemv_batched", x2.data_ptr(), _dtype_id(x2, "x"), m, in_f, int(out_features),
+                  tp.data_ptr(), sp.data_ptr(), vp.data_ptr(), tp.numel(), idx.data_ptr(), e, K, cb,
+                  out.data_ptr(), _DTYPE_ID[torch.float16], ws.data_ptr(), ws.numel(), stream_of(dev))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Routed-expert MoE
 # ---------------------------------------------------------------------------
