@@ -222,15 +222,53 @@ int exl3_kv_decode(const void* q, int q_dtype, int64_t B, int64_t Hq, int64_t nu
                    int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * The reference's NVFP4 ("q4") paged KV cache, byte for byte: pool uint8
+ * [pages][2*H][128][72] (slot 2h = K, 2h+1 = V of KV head h; a slot is a flat
+ * 9216-byte region of 128 x 64 e2m1 data bytes then 1024 e4m3 scale bytes,
+ * K scales linear, V scales token-quad swizzled).
+ *   pack: k, v [B, H, L, 128] (dtype 0 fp16, 1 bf16, 2 fp32; element strides
+ *     stride_b/h/t, unit dim stride); token p < seq_lens[b] of sequence b goes
+ *     to slot p % 128 of page block_table[b * bt_stride + p / 128].  Replaces
+ *     pack_q4_row / pack_slot_region_side (src/vllm_exl3/
+ *     minimax_q4kv_reference.py:297-366); bit-exact.
+ *   dequant: out fp32 [pages][2H][128][128].  Replaces dequant_pool_pages
+ *     (minimax_q4kv_reference.py:735-776).
+ *   sparse decode: q [total_q, Hq, 128] (strides q_stride_n/h), topk_idx
+ *     int32 [Hkv][total_q][topk] (strides topk_stride_h/n, unit last stride)
+ *     of logical block ids, block_table int32 [num_reqs][max_blocks],
+ *     seq_lens int32 [num_reqs], total_q = num_reqs * decode_query_len;
+ *     n_chunks splits of the top-k list, merged by log-sum-exp; out as q.
+ *     Replaces q4_sparse_decode + _q4_decode_kernel
+ *     (src/vllm_exl3/minimax_q4kv_kernels.py:385-506, 772-877). */
+int64_t exl3_nvfp4_page_bytes(int64_t num_kv_heads);
+int exl3_nvfp4_pack_pages(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                          int64_t stride_b, int64_t stride_h, int64_t stride_t, int64_t max_len,
+                          const int32_t* seq_lens, const int32_t* block_table, int64_t bt_stride,
+                          int64_t max_blocks, void* pool, int64_t num_pages, void* stream);
+int exl3_nvfp4_dequant_pages(const void* pool, int64_t num_pages, int64_t H, float* out,
+                             void* stream);
+int64_t exl3_nvfp4_decode_workspace_size(int64_t total_q, int64_t Hq, int64_t n_chunks);
+int exl3_nvfp4_sparse_decode(const void* q, int q_dtype, int64_t total_q, int64_t Hq, int64_t Hkv,
+                             int64_t q_stride_n, int64_t q_stride_h, const void* pool,
+                             int64_t num_pages, const int32_t* topk_idx, int64_t topk_stride_h,
+                             int64_t topk_stride_n, int64_t max_topk, const int32_t* block_table,
+                             int64_t bt_stride, int64_t max_blocks, const int32_t* seq_lens,
+                             int64_t decode_query_len, float sm_scale, void* out, int out_dtype,
+                             int64_t out_stride_n, int64_t out_stride_h, int64_t n_chunks,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Instrumentation (no counterpart in the reference; used by the benchmark to
  * time individual kernels on their launch stream).  Between begin and end,
  * every instrumented call records HIP events at its phase boundaries:
- *   exl3_moe_forward: 0 route | 1 gate/up GEMV | 2 down GEMV | 3 combine
- *   exl3_gemm:        0 GEMV | 1 split finish (when split)
+ *   exl3_moe_forward: 0 route | 1 input rotation | 2 gate/up GEMV | 3 gate/up
+ *                     finish + activation | 4 down GEMV | 5 combine
+ *   exl3_gemm:        0 input rotation | 1 GEMV | 2 split finish (when split)
  *   exl3_moe_prefill: 0 route | 1 input rotation | 2 gate/up GEMMs | 3 activation
  *                     | 4 down GEMM | 5 combine
  *   exl3_fat_gemm{,_scatter}: 0 GEMM | 1 output rotation (+ scatter)
  *   exl3_kv_decode:   0 split-K attention | 1 merge
+ *   exl3_nvfp4_sparse_decode: 0 block-sparse attention | 1 merge
  * Recording never synchronises.  exl3_profile_end waits for the events and
  * writes, per phase, the summed elapsed milliseconds over the recorded calls
  * (at most max_calls are recorded).  Not thread-safe. */

@@ -1,0 +1,526 @@
+// The reference's NVFP4 ("q4") paged KV cache on gfx950: page pack, pool
+// dequant and the block-sparse split decode attention with its merge.
+//
+// Replaces src/vllm_exl3/minimax_q4kv_reference.py (pack_q4_row :297-326,
+// pack_slot_region_side :352-366, dequant_pool_pages :735-776) and the decode
+// overlay q4_sparse_decode + _q4_decode_kernel
+// (src/vllm_exl3/minimax_q4kv_kernels.py:385-506, 772-877).  Format (kept
+// byte for byte, it is the pool the model writes): 128-token pages, slot
+// 2h + side (K 0, V 1) of a page is a flat 9216-byte region, data
+// [128 tokens][64 B] (byte j of a token = e2m1 nibbles of dims 2j, 2j+1, low
+// nibble even) then 1024 scale bytes (e4m3 per 16 dims; K linear t*8+g, V
+// the 4x4 token-quad swizzle).
+//
+// Pack: one wave per (token, KV head, side) row, lane l owns dims 2l, 2l+1
+// (one data byte).  bf16 rounding, group max over 8 lanes, s = max(amax/6,
+// 2^-9) as saturating RNE e4m3, q = RZ(x * RN(1/s)) (the RN product, stepped
+// toward zero when fma shows it rounded away), RNE e2m1 codes with the
+// reference's tie rules.  Bit-exact with the reference packer.
+//
+// Decode: one 256-thread workgroup per (query token, KV head, chunk of the
+// top-k list).  Per listed block: the K and V slots are dequantised into LDS
+// as fp16 (e2m1 x e4m3 is exact in fp16) with v_cvt_scalef32_pk_f16_fp4 and
+// one packed multiply per pair; scores, the online softmax (log2 domain) and
+// P.V run in fp32.  The chunk's normalised output and its log2-sum-exp go
+// to a workspace; the merge kernel combines the chunks.
+#include "exl3_common.h"
+#include "profile.h"
+
+#include <cmath>
+
+namespace exl3 {
+namespace {
+
+constexpr int kQ4Page = 128;
+constexpr int kQ4Dim = 128;
+constexpr int kQ4Slot = 9216;
+constexpr int kQ4Data = 8192;
+constexpr int kQ4MaxGroup = 16;   // query heads per KV head
+constexpr int kQ4Threads = 256;
+constexpr int kQ4Pitch = kQ4Dim + 8;  // fp16 LDS row pitch (bank spread)
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float q4_load(const void* x, int dtype, int64_t idx) {
+    if (dtype == 2) return reinterpret_cast<const float*>(x)[idx];
+    const uint16_t b = reinterpret_cast<const uint16_t*>(x)[idx];
+    if (dtype == 0) return (float)bits_to_half(b);
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+// fp32 -> bf16 (RNE) -> fp32; NaN becomes the canonical +NaN, as torch's
+// float -> bfloat16 cast does (a bf16 input is not converted at all).
+__device__ __forceinline__ float bf16_round(float x) {
+    if (x != x) return __builtin_bit_cast(float, 0x7FC00000u);
+    uint32_t b = __builtin_bit_cast(uint32_t, x);
+    b = (b + 0x7FFFu + ((b >> 16) & 1u)) & 0xFFFF0000u;
+    return __builtin_bit_cast(float, b);
+}
+
+// Saturating RNE fp32 -> e4m3fn byte; NaN -> 0x7F with its sign.
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+    const uint32_t sign = __builtin_bit_cast(uint32_t, x) >> 31;
+    if (x != x) return 0x7Fu | (sign << 7);
+    const float ax = fabsf(x);
+    const uint32_t bits = __builtin_bit_cast(uint32_t, ax);
+    int e8 = (int)((bits >> 23) & 0xFF) - 120;
+    uint32_t man = bits & 0x7FFFFFu;
+    uint32_t code;
+    if (e8 <= 0) {
+        // subnormal: round(ax * 512) to nearest even; 8 becomes code 0x08
+        const float t = ax * 512.0f;  // exact scaling
+        const float fl = floorf(t);
+        const float frac = t - fl;
+        const uint32_t fi = (uint32_t)fl;
+        const uint32_t inc = (frac > 0.5f || (frac == 0.5f && (fi & 1u))) ? 1u : 0u;
+        code = fi + inc;
+    } else {
+        uint32_t m3 = man >> 20;
+        const uint32_t rest = man & 0xFFFFFu;
+        if (rest > 0x80000u || (rest == 0x80000u && (m3 & 1u))) ++m3;
+        if (m3 == 8) {
+            m3 = 0;
+            ++e8;
+        }
+        code = (e8 >= 1 && e8 <= 15 && !(e8 == 15 && m3 == 7)) ? (((uint32_t)e8 << 3) | m3) : 0x7Eu;
+    }
+    return (code | (sign << 7)) & 0xFFu;
+}
+
+__device__ __forceinline__ float e4m3_value(uint32_t b) {
+    return __builtin_amdgcn_cvt_f32_fp8((int)b, 0);  // OCP e4m3fn (checked on gfx950)
+}
+
+// e2m1 code 0..7 of |q| (RNE with the reference's ties); NaN -> 7
+__device__ __forceinline__ uint32_t e2m1_code(float a) {
+    if (a != a) return 7;
+    return (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.0f);
+}
+
+// RZ at fp32 of the exact product x * r
+__device__ __forceinline__ float rz_mul(float x, float r) {
+    const float p = x * r;
+    const float e = __builtin_fmaf(x, r, -p);  // exact remainder
+    if (p != 0.0f && e != 0.0f && (__builtin_bit_cast(uint32_t, e) ^ __builtin_bit_cast(uint32_t, p)) >> 31 &&
+        __builtin_isfinite(p))
+        return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, p) - 1u);  // one step toward 0
+    return p;
+}
+
+__device__ __forceinline__ int scale_offset(int side, int t, int g) {
+    if (side == 0) return t * 8 + g;
+    return ((t >> 2) * 4 + (g >> 1)) * 8 + (g & 1) * 4 + (t & 3);
+}
+
+struct Q4PackParams {
+    const void* k;
+    const void* v;
+    int dtype;
+    int B, H;
+    int64_t sb, sh, st;        // element strides of k/v [B, H, L, 128]
+    const int* seq_lens;
+    const int* block_table;
+    int64_t bt_stride;
+    int max_blocks;
+    int max_len;
+    uint8_t* pool;             // [pages][2H][9216]
+    int64_t num_pages;
+};
+
+__global__ __launch_bounds__(256) void q4_pack_kernel(Q4PackParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    // unit = ((b * max_len + pos) * H + h) * 2 + side
+    const int side = (int)(unit & 1);
+    const int64_t r = unit >> 1;
+    const int h = (int)(r % p.H);
+    const int64_t bp = r / p.H;
+    const int pos = (int)(bp % p.max_len);
+    const int b = (int)(bp / p.max_len);
+    if (b >= p.B || pos >= p.seq_lens[b]) return;  // wave-uniform
+    const int blk = pos / kQ4Page, t = pos % kQ4Page;
+    if (blk >= p.max_blocks) return;
+    const int64_t page = p.block_table[(int64_t)b * p.bt_stride + blk];
+    if (page < 0 || page >= p.num_pages) return;
+    const void* x = side ? p.v : p.k;
+    const int64_t base = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)pos * p.st + 2 * lane;
+    float x0 = q4_load(x, p.dtype, base), x1 = q4_load(x, p.dtype, base + 1);
+    if (p.dtype != 1) {  // bf16 inputs are already bf16 values
+        x0 = bf16_round(x0);
+        x1 = bf16_round(x1);
+    }
+    // group of 16 dims = 8 lanes; amax ignores NaN (hardware fmax)
+    float am = fmaxf(x0 != x0 ? 0.0f : fabsf(x0), x1 != x1 ? 0.0f : fabsf(x1));
+    am = fmaxf(am, __shfl_xor(am, 1, 64));
+    am = fmaxf(am, __shfl_xor(am, 2, 64));
+    am = fmaxf(am, __shfl_xor(am, 4, 64));
+    const float s = fmaxf(am / 6.0f, 0.001953125f);  // 2^-9
+    const uint32_t sb = e4m3_encode(s);
+    const float recip = 1.0f / e4m3_value(sb);
+    uint32_t nib[2];
+    const float xs[2] = {x0, x1};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float q = rz_mul(xs[i], recip);
+        const uint32_t c = e2m1_code(fabsf(q));
+        nib[i] = c == 0 ? 0u : (c | ((__builtin_bit_cast(uint32_t, q) >> 31) << 3));
+    }
+    uint8_t* region = p.pool + (page * (2 * p.H) + 2 * h + side) * (int64_t)kQ4Slot;
+    region[t * 64 + lane] = (uint8_t)(nib[0] | (nib[1] << 4));
+    if ((lane & 7) == 0) region[kQ4Data + scale_offset(side, t, lane >> 3)] = (uint8_t)sb;
+}
+
+// Pool -> fp32 values [pages][2H][128][128]; one thread per data byte.
+__global__ __launch_bounds__(256) void q4_dequant_kernel(const uint8_t* pool, int64_t n_slots,
+                                                         float* out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // byte index over all slots
+    if (i >= n_slots * kQ4Data) return;
+    const int64_t slot = i / kQ4Data;
+    const int j = (int)(i % kQ4Data);
+    const int t = j >> 6, byte = j & 63;
+    const uint8_t* region = pool + slot * kQ4Slot;
+    const int side = (int)(slot & 1);
+    const float sc = e4m3_value(region[kQ4Data + scale_offset(side, t, byte >> 3)]);
+    const h2v v = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4((uint32_t)region[j], 1.0f, 0);
+    float* o = out + slot * (kQ4Page * kQ4Dim) + t * kQ4Dim + 2 * byte;
+    o[0] = (float)v[0] * sc;
+    o[1] = (float)v[1] * sc;
+}
+
+struct Q4DecodeParams {
+    const void* q;
+    int q_dtype;
+    int total_q, Hq, Hkv, G;
+    int64_t q_sn, q_sh;
+    const uint8_t* pool;
+    int64_t num_pages;
+    const int* topk;           // [Hkv][total_q][max_topk] (strides below)
+    int64_t tk_sh, tk_sn;
+    int max_topk;
+    const int* block_table;
+    int64_t bt_stride;
+    int max_blocks;
+    const int* seq_lens;
+    int dql;                   // decode_query_len
+    float scale_log2;          // sm_scale * log2(e)
+    int n_chunks;
+    float* o_part;             // [chunks][total_q][Hq][128]
+    float* lse_part;           // [chunks][total_q][Hq]
+};
+
+// Dequantise one 9216-byte slot into LDS as fp16 [128][kQ4Pitch]; thread
+// tid handles token tid/2, dims [64 (tid & 1), +64).
+__device__ __forceinline__ void stage_slot(const uint8_t* region, int side, uint16_t* lds, int tid) {
+    const int t = tid >> 1, half = tid & 1;
+    const u32x4* src = reinterpret_cast<const u32x4*>(region + t * 64 + 32 * half);
+    const u32x4 d0 = src[0], d1 = src[1];
+    uint32_t w[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    uint32_t* dst = reinterpret_cast<uint32_t*>(lds + t * kQ4Pitch + 64 * half);
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {  // groups 4 half + gi (16 dims = 2 words)
+        const float sc = e4m3_value(region[kQ4Data + scale_offset(side, t, 4 * half + gi)]);
+        const h2v s2 = {(_Float16)sc, (_Float16)sc};
+#pragma unroll
+        for (int wi = 0; wi < 2; ++wi) {
+            const uint32_t word = w[2 * gi + wi];
+#pragma unroll
+            for (int by = 0; by < 4; ++by) {
+                h2v v = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word >> (8 * by), 1.0f, 0);
+                v = v * s2;  // exact: e2m1 x e4m3 fits fp16
+                dst[(2 * gi + wi) * 4 + by] = __builtin_bit_cast(uint32_t, v);
+            }
+        }
+    }
+}
+
+struct Q4Lds {
+    uint16_t K[kQ4Page * kQ4Pitch];
+    uint16_t V[kQ4Page * kQ4Pitch];
+    float q[kQ4MaxGroup][kQ4Dim];
+    float p[kQ4MaxGroup][kQ4Page];
+    float red[kQ4MaxGroup][4];
+    float m[kQ4MaxGroup], l[kQ4MaxGroup], alpha[kQ4MaxGroup];
+};
+
+__global__ __launch_bounds__(kQ4Threads) void q4_decode_kernel(Q4DecodeParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
+    Q4Lds& L = *reinterpret_cast<Q4Lds*>(q4_lds);
+    uint16_t* Ks = L.K;
+    uint16_t* Vs = L.V;
+    float (*qs)[kQ4Dim] = L.q;
+    float (*ps)[kQ4Page] = L.p;
+    float (*red)[4] = L.red;
+    float* m_s = L.m;
+    float* l_s = L.l;
+    float* alpha_s = L.alpha;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = blockIdx.x % p.total_q;
+    const int c = blockIdx.x / p.total_q;
+    const int h = blockIdx.y;
+    const int G = p.G;
+    const int req = i / p.dql;
+    const int qpos = p.seq_lens[req] - p.dql + (i - req * p.dql);
+    const int kv_len = max(qpos + 1, 0);
+    const int n_blocks = (kv_len + kQ4Page - 1) / kQ4Page;
+    const int real_topk = min(p.max_topk, n_blocks);
+    const int chunk = (p.max_topk + p.n_chunks - 1) / p.n_chunks;
+    const int c0 = c * chunk, c1 = min(c0 + chunk, real_topk);
+
+    for (int e = tid; e < G * kQ4Dim; e += kQ4Threads) {
+        const int hh = e / kQ4Dim, d = e % kQ4Dim;
+        qs[hh][d] = q4_load(p.q, p.q_dtype, (int64_t)i * p.q_sn + (int64_t)(h * G + hh) * p.q_sh + d) *
+                    p.scale_log2;
+    }
+    if (tid < kQ4MaxGroup) {
+        m_s[tid] = -INFINITY;
+        l_s[tid] = 0.0f;
+    }
+    // thread tid accumulates O[hh][d] for d = tid % 128, heads tid/128, +2, ...
+    const int od = tid & 127, oh0 = tid >> 7;
+    float acc[kQ4MaxGroup / 2];
+#pragma unroll
+    for (int k = 0; k < kQ4MaxGroup / 2; ++k) acc[k] = 0.0f;
+    const int* tk = p.topk + (int64_t)h * p.tk_sh + (int64_t)i * p.tk_sn;
+    const int* bt = p.block_table + (int64_t)req * p.bt_stride;
+
+    for (int e = c0; e < c1; ++e) {
+        const int blk = tk[e];
+        if (blk < 0 || blk >= n_blocks) continue;  // uniform
+        const int64_t page = bt[blk];
+        if (page < 0 || page >= p.num_pages) continue;
+        const uint8_t* base = p.pool + (page * (2 * p.Hkv) + 2 * h) * (int64_t)kQ4Slot;
+        __syncthreads();  // previous block's LDS reads are done
+        stage_slot(base, 0, Ks, tid);
+        stage_slot(base + kQ4Slot, 1, Vs, tid);
+        __syncthreads();
+        const int n_tok = min(kQ4Page, kv_len - blk * kQ4Page);
+        // scores (log2 domain): thread -> token tid % 128, heads tid/128, +2, ...
+        const int t = tid & 127;
+        float bmax[kQ4MaxGroup / 2];
+#pragma unroll
+        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
+            const int hh = oh0 + 2 * k;
+            float sc = -INFINITY;
+            if (hh < G && t < n_tok) {
+                float s = 0.0f;
+                const uint32_t* kr = reinterpret_cast<const uint32_t*>(Ks + t * kQ4Pitch);
+#pragma unroll 8
+                for (int d2 = 0; d2 < kQ4Dim / 2; ++d2) {
+                    const h2v kv = __builtin_bit_cast(h2v, kr[d2]);
+                    s = __builtin_fmaf(qs[hh][2 * d2], (float)kv[0], s);
+                    s = __builtin_fmaf(qs[hh][2 * d2 + 1], (float)kv[1], s);
+                }
+                sc = s;
+            }
+            if (hh < G) ps[hh][t] = sc;
+            bmax[k] = sc;
+        }
+        // block max per head: wave reduction then across the two waves of a head
+#pragma unroll
+        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
+            float v = bmax[k];
+            for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+            const int hh = oh0 + 2 * k;
+            if (lane == 0 && hh < G) red[hh][wave & 1] = v;
+        }
+        __syncthreads();
+        if (tid < G) {
+            const float mb = fmaxf(red[tid][0], red[tid][1]);
+            const float mn = fmaxf(m_s[tid], mb);
+            alpha_s[tid] = exp2f(m_s[tid] - mn);  // 0 when the old max is -inf
+            m_s[tid] = mn;
+        }
+        __syncthreads();
+        // probabilities and their sums
+        float bsum[kQ4MaxGroup / 2];
+#pragma unroll
+        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
+            const int hh = oh0 + 2 * k;
+            float pv = 0.0f;
+            if (hh < G) {
+                const float sc = ps[hh][t];
+                pv = sc == -INFINITY ? 0.0f : exp2f(sc - m_s[hh]);
+                ps[hh][t] = pv;
+            }
+            bsum[k] = pv;
+        }
+#pragma unroll
+        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
+            float v = bsum[k];
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            const int hh = oh0 + 2 * k;
+            if (lane == 0 && hh < G) red[hh][2 + (wave & 1)] = v;
+        }
+        __syncthreads();
+        if (tid < G) l_s[tid] = l_s[tid] * alpha_s[tid] + red[tid][2] + red[tid][3];
+        // P.V: thread -> dim od, heads oh0, +2, ...
+#pragma unroll
+        for (int k = 0; k < kQ4MaxGroup / 2; ++k)
+            if (oh0 + 2 * k < G) acc[k] *= alpha_s[oh0 + 2 * k];
+        for (int tt = 0; tt < n_tok; ++tt) {
+            const float vv = (float)__builtin_bit_cast(_Float16, Vs[tt * kQ4Pitch + od]);
+#pragma unroll
+            for (int k = 0; k < kQ4MaxGroup / 2; ++k)
+                if (oh0 + 2 * k < G) acc[k] = __builtin_fmaf(ps[oh0 + 2 * k][tt], vv, acc[k]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
+        const int hh = oh0 + 2 * k;
+        if (hh < G) {
+            const float l = l_s[hh];
+            const int64_t o = ((int64_t)c * p.total_q + i) * p.Hq + h * G + hh;
+            p.o_part[o * kQ4Dim + od] = l > 0.0f ? acc[k] / l : 0.0f;
+            if (od == 0) p.lse_part[o] = l > 0.0f ? m_s[hh] + log2f(l) : -INFINITY;
+        }
+    }
+}
+
+// out[i][head][d] = sum_c o_c * 2^(lse_c - M) / sum_c 2^(lse_c - M); zero
+// when no chunk saw a token.  One thread per (i, head, d).
+__global__ __launch_bounds__(256) void q4_merge_kernel(const float* o_part, const float* lse_part,
+                                                       int n_chunks, int total_q, int Hq, void* out,
+                                                       int out_dtype, int64_t o_sn, int64_t o_sh) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)total_q * Hq * kQ4Dim) return;
+    const int d = (int)(idx % kQ4Dim);
+    const int64_t ih = idx / kQ4Dim;
+    const int head = (int)(ih % Hq), i = (int)(ih / Hq);
+    const int64_t stride = (int64_t)total_q * Hq;
+    float M = -INFINITY;
+    for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, lse_part[c * stride + ih]);
+    float num = 0.0f, den = 0.0f;
+    if (M > -INFINITY) {
+        for (int c = 0; c < n_chunks; ++c) {
+            const float w = exp2f(lse_part[c * stride + ih] - M);
+            num += w * o_part[(c * stride + ih) * kQ4Dim + d];
+            den += w;
+        }
+    }
+    const float v = den > 0.0f ? num / den : 0.0f;
+    const int64_t o = (int64_t)i * o_sn + (int64_t)head * o_sh + d;
+    if (out_dtype == 2)
+        reinterpret_cast<float*>(out)[o] = v;
+    else if (out_dtype == 0)
+        reinterpret_cast<uint16_t*>(out)[o] = half_to_bits((half_t)v);
+    else {
+        uint32_t b = __builtin_bit_cast(uint32_t, v);
+        b += 0x7FFFu + ((b >> 16) & 1u);
+        reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)(b >> 16);
+    }
+}
+
+}  // namespace
+}  // namespace exl3
+
+using namespace exl3;
+
+EXL3_API int64_t exl3_nvfp4_page_bytes(int64_t num_kv_heads) {
+    return num_kv_heads > 0 ? 2 * num_kv_heads * (int64_t)kQ4Slot : 0;
+}
+
+EXL3_API int exl3_nvfp4_pack_pages(const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                                   int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                                   int64_t max_len, const int32_t* seq_lens,
+                                   const int32_t* block_table, int64_t bt_stride,
+                                   int64_t max_blocks, void* pool, int64_t num_pages, void* stream) {
+    EXL3_CHECK(dtype >= 0 && dtype <= 2, "dtype ids: 0 fp16, 1 bf16, 2 fp32");
+    EXL3_CHECK(B >= 1 && H >= 1 && max_len >= 1 && max_blocks >= 1 && num_pages >= 1,
+               "q4 pack: empty geometry");
+    EXL3_CHECK(B * max_len * H * 2 < (1ll << 40), "q4 pack: too many rows");
+    EXL3_CHECK(k && v && seq_lens && block_table && pool, "null pointer argument");
+    Q4PackParams p = {k, v, dtype, (int)B, (int)H, stride_b, stride_h, stride_t,
+                      seq_lens, block_table, bt_stride, (int)max_blocks, (int)max_len,
+                      reinterpret_cast<uint8_t*>(pool), num_pages};
+    const int64_t units = B * max_len * H * 2;
+    q4_pack_kernel<<<(unsigned)((units + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(p);
+    EXL3_LAUNCHED();
+    return kOk;
+}
+
+EXL3_API int exl3_nvfp4_dequant_pages(const void* pool, int64_t num_pages, int64_t H, float* out,
+                                      void* stream) {
+    EXL3_CHECK(num_pages >= 1 && H >= 1 && pool && out, "q4 dequant: bad arguments");
+    const int64_t n_slots = num_pages * 2 * H;
+    const int64_t bytes = n_slots * kQ4Data;
+    q4_dequant_kernel<<<(unsigned)((bytes + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        reinterpret_cast<const uint8_t*>(pool), n_slots, out);
+    EXL3_LAUNCHED();
+    return kOk;
+}
+
+EXL3_API int64_t exl3_nvfp4_decode_workspace_size(int64_t total_q, int64_t Hq, int64_t n_chunks) {
+    if (total_q < 1 || Hq < 1 || n_chunks < 1) return 0;
+    return (int64_t)(((size_t)n_chunks * total_q * Hq * (kQ4Dim + 1) * 4 + 255) & ~(size_t)255);
+}
+
+EXL3_API int exl3_nvfp4_sparse_decode(const void* q, int q_dtype, int64_t total_q, int64_t Hq,
+                                      int64_t Hkv, int64_t q_stride_n, int64_t q_stride_h,
+                                      const void* pool, int64_t num_pages, const int32_t* topk_idx,
+                                      int64_t topk_stride_h, int64_t topk_stride_n,
+                                      int64_t max_topk, const int32_t* block_table,
+                                      int64_t bt_stride, int64_t max_blocks,
+                                      const int32_t* seq_lens, int64_t decode_query_len,
+                                      float sm_scale, void* out, int out_dtype,
+                                      int64_t out_stride_n, int64_t out_stride_h, int64_t n_chunks,
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
+    EXL3_CHECK(q_dtype >= 0 && q_dtype <= 2 && out_dtype >= 0 && out_dtype <= 2,
+               "dtype ids: 0 fp16, 1 bf16, 2 fp32");
+    EXL3_CHECK(total_q >= 1 && Hkv >= 1 && Hq % Hkv == 0 && Hq / Hkv <= kQ4MaxGroup,
+               "q4 decode: Hq must be a multiple of num_kv_heads, at most 16 per KV head");
+    EXL3_CHECK(max_topk >= 1 && decode_query_len >= 1 && total_q % decode_query_len == 0 &&
+                   n_chunks >= 1 && max_blocks >= 1 && num_pages >= 1,
+               "q4 decode: bad geometry");
+    EXL3_CHECK(std::isfinite(sm_scale), "q4 decode: sm_scale must be finite");
+    EXL3_CHECK(q && pool && topk_idx && block_table && seq_lens && out, "null pointer argument");
+    const int64_t need = exl3_nvfp4_decode_workspace_size(total_q, Hq, n_chunks);
+    EXL3_CHECK(workspace && workspace_bytes >= need, "workspace too small: need %lld bytes",
+               (long long)need);
+    Q4DecodeParams p;
+    p.q = q;
+    p.q_dtype = q_dtype;
+    p.total_q = (int)total_q;
+    p.Hq = (int)Hq;
+    p.Hkv = (int)Hkv;
+    p.G = (int)(Hq / Hkv);
+    p.q_sn = q_stride_n;
+    p.q_sh = q_stride_h;
+    p.pool = reinterpret_cast<const uint8_t*>(pool);
+    p.num_pages = num_pages;
+    p.topk = topk_idx;
+    p.tk_sh = topk_stride_h;
+    p.tk_sn = topk_stride_n;
+    p.max_topk = (int)max_topk;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.max_blocks = (int)max_blocks;
+    p.seq_lens = seq_lens;
+    p.dql = (int)decode_query_len;
+    p.scale_log2 = sm_scale * 1.4426950408889634f;
+    p.n_chunks = (int)n_chunks;
+    p.o_part = reinterpret_cast<float*>(workspace);
+    p.lse_part = p.o_part + (size_t)n_chunks * total_q * Hq * kQ4Dim;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    static const hipError_t lds_ok = [] {
+        hipError_t e = hipFuncSetAttribute((const void*)q4_decode_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Q4Lds));
+        if (e != hipSuccess) (void)hipGetLastError();
+        return e;
+    }();
+    EXL3_HIP(lds_ok);
+    profile_begin_call();
+    profile_mark(0, st);
+    q4_decode_kernel<<<dim3((unsigned)(total_q * n_chunks), (unsigned)Hkv), kQ4Threads, sizeof(Q4Lds),
+                       st>>>(p);
+    EXL3_LAUNCHED();
+    profile_mark(1, st);
+    const int64_t n = total_q * Hq * kQ4Dim;
+    q4_merge_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.o_part, p.lse_part, (int)n_chunks,
+                                                               (int)total_q, (int)Hq, out, out_dtype,
+                                                               out_stride_n, out_stride_h);
+    EXL3_LAUNCHED();
+    profile_mark(2, st);
+    return kOk;
+}

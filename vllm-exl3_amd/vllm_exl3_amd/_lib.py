@@ -48,12 +48,21 @@ SIGNATURES: dict[str, list] = {
     "exl3_kv_decode_workspace_size": [_i64, _i64, _i64, _i64, _i64],
     "exl3_kv_decode": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _f32,
                        _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
+    "exl3_nvfp4_page_bytes": [_i64],
+    "exl3_nvfp4_pack_pages": [_p, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64,
+                              _p, _i64, _p],
+    "exl3_nvfp4_dequant_pages": [_p, _i64, _i64, _p, _p],
+    "exl3_nvfp4_decode_workspace_size": [_i64, _i64, _i64],
+    "exl3_nvfp4_sparse_decode": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64,
+                                 _i64, _p, _i64, _i64, _p, _i64, _f32, _p, _i32, _i64, _i64, _i64,
+                                 _p, _i64, _p],
     "exl3_profile_begin": [_i32],
     "exl3_profile_end": [_p, _i32, _p, _p],
 }
 _RESTYPES = {"exl3_last_error": ctypes.c_char_p, "exl3_gemm_workspace_size": _i64,
              "exl3_moe_workspace_size": _i64, "exl3_fat_gemm_workspace_size": _i64,
              "exl3_gemv_batched_workspace_size": _i64,
+             "exl3_nvfp4_page_bytes": _i64, "exl3_nvfp4_decode_workspace_size": _i64,
              "exl3_moe_prefill_workspace_size": _i64, "exl3_kv_page_bytes": _i64,
              "exl3_kv_decode_workspace_size": _i64}
 

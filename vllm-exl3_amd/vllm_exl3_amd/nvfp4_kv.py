@@ -1,0 +1,140 @@
+"""The reference's NVFP4 ("q4") paged KV cache on the GPU: pack, pool
+dequant and the block-sparse decode attention.
+
+Host side of ``q4_sparse_decode`` (src/vllm_exl3/minimax_q4kv_kernels.py:
+772-877) and of the reference packer / dequantiser
+(src/vllm_exl3/minimax_q4kv_reference.py:297-366, 735-776) over the same
+pool format, byte for byte: uint8 ``[pages, 2*num_kv_heads, 128, 72]``,
+slot ``2h`` = K and ``2h+1`` = V of KV head h, each slot a flat 9216-byte
+region (128 tokens x 64 data bytes, then 1024 e4m3 scale bytes).  Every call
+runs the HIP kernels of ``libexl3_mi355x.so``; there is no CPU path.
+Geometry errors raise ``ValueError`` before any launch; nothing synchronises
+with the host, so a decode step can be captured in a HIP graph.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .vllm_exl3_c import _DTYPE_ID, stream_of, workspace
+
+PAGE_TOKENS = 128
+HEAD_DIM = 128
+ROW_BYTES = 72
+
+
+def new_pool(num_pages: int, num_kv_heads: int, device) -> torch.Tensor:
+    """A zeroed pool uint8 [num_pages, 2*num_kv_heads, 128, 72]."""
+    return torch.zeros((num_pages, 2 * num_kv_heads, PAGE_TOKENS, ROW_BYTES), dtype=torch.uint8,
+                       device=device)
+
+
+def _check_pool(pool: torch.Tensor, num_kv_heads: int | None = None) -> None:
+    if pool.dtype is not torch.uint8:
+        raise ValueError("q4 decode requires the pool as raw uint8 bytes")
+    if pool.dim() != 4 or pool.shape[2:] != (PAGE_TOKENS, ROW_BYTES) or pool.shape[1] % 2:
+        raise ValueError("q4 pool geometry mismatch")
+    if num_kv_heads is not None and pool.shape[1] != 2 * num_kv_heads:
+        raise ValueError("q4 pool geometry mismatch")
+    if pool.stride(3) != 1 or pool.stride(2) != ROW_BYTES or pool.stride(1) != PAGE_TOKENS * ROW_BYTES \
+            or pool.stride(0) != pool.shape[1] * PAGE_TOKENS * ROW_BYTES:
+        raise ValueError("q4 pool slot regions must be contiguous")
+    if not pool.is_cuda:
+        raise ValueError("the q4 pool lives in device memory")
+
+
+def _i32(t: torch.Tensor, name: str, device) -> torch.Tensor:
+    if t.dtype not in (torch.int32, torch.int64) or t.device != device:
+        raise ValueError(f"{name} must be an int32/int64 tensor on the pool's device")
+    return t.to(torch.int32)
+
+
+def pack_pages(k: torch.Tensor, v: torch.Tensor, seq_lens: torch.Tensor,
+               block_table: torch.Tensor, pool: torch.Tensor) -> None:
+    """Quantise k, v [B, kv_heads, L, 128] (fp16/bf16/fp32, unit dim stride)
+    into the pool: token p of sequence b goes to slot p % 128 of page
+    block_table[b, p // 128]; only tokens [0, seq_lens[b]) are written."""
+    _check_pool(pool)
+    if k.shape != v.shape or k.dim() != 4 or k.size(3) != HEAD_DIM:
+        raise ValueError("k and v must both be [B, kv_heads, L, 128]")
+    if k.stride() != v.stride() or k.stride(3) != 1 or k.dtype != v.dtype or k.dtype not in _DTYPE_ID:
+        raise ValueError("k and v must share a float dtype and strides, with unit dim stride")
+    B, H, L, _ = k.shape
+    if pool.shape[1] != 2 * H or k.device != pool.device or v.device != pool.device:
+        raise ValueError("k/v geometry does not match the pool")
+    sl = _i32(seq_lens, "seq_lens", pool.device).contiguous()
+    bt = _i32(block_table, "block_table", pool.device)
+    if sl.numel() != B or bt.dim() != 2 or bt.size(0) != B or bt.stride(1) != 1:
+        raise ValueError("seq_lens [B] and block_table [B, max_blocks] (unit column stride) required")
+    with torch.cuda.device(pool.device):
+        _lib.call("exl3_nvfp4_pack_pages", k.data_ptr(), v.data_ptr(), _DTYPE_ID[k.dtype], B, H,
+                  k.stride(0), k.stride(1), k.stride(2), L, sl.data_ptr(), bt.data_ptr(), bt.stride(0),
+                  bt.size(1), pool.data_ptr(), pool.size(0), stream_of(pool.device))
+
+
+def dequant_pool_pages(pool: torch.Tensor) -> torch.Tensor:
+    """fp32 values [pages, 2*kv_heads, 128, 128] of every slot
+    (``dequant_pool_pages``, minimax_q4kv_reference.py:735-776)."""
+    _check_pool(pool)
+    out = torch.empty((pool.size(0), pool.size(1), PAGE_TOKENS, HEAD_DIM), dtype=torch.float32,
+                      device=pool.device)
+    with torch.cuda.device(pool.device):
+        _lib.call("exl3_nvfp4_dequant_pages", pool.data_ptr(), pool.size(0), pool.size(1) // 2,
+                  out.data_ptr(), stream_of(pool.device))
+    return out
+
+
+def _chunks(total_q: int, num_kv_heads: int, max_topk: int) -> int:
+    """Shape-constant number of top-k chunks (graph safe): about 512
+    workgroups in flight, a power of two, at most max_topk."""
+    target = max(1, min(max_topk, 512 // max(1, total_q * num_kv_heads)))
+    return 1 << (target.bit_length() - 1)
+
+
+def q4_sparse_decode(q: torch.Tensor, pool: torch.Tensor, topk_idx: torch.Tensor,
+                     block_table: torch.Tensor, seq_lens: torch.Tensor, num_kv_heads: int,
+                     sm_scale: float, output: torch.Tensor, decode_query_len: int) -> None:
+    """Block-sparse decode attention over the q4 pool, written into
+    ``output`` [total_q, H, 128].  Same arguments and meaning as the
+    reference: topk_idx [num_kv_heads, total_q, topk] logical block ids per
+    query token (entries outside [0, n_blocks) skipped; the first
+    min(topk, n_blocks) entries are examined), causal within the last block,
+    query token i of request i // decode_query_len at position
+    seq_len - decode_query_len + i % decode_query_len."""
+    if q.dim() != 3 or q.size(2) != HEAD_DIM or q.stride(2) != 1:
+        raise ValueError("q4 decode requires head_dim == 128")
+    _check_pool(pool, num_kv_heads)
+    total_q, Hq, _ = q.shape
+    if Hq % num_kv_heads or Hq // num_kv_heads > 16:
+        raise ValueError("q4 decode: Hq must be a multiple of num_kv_heads, at most 16 per KV head")
+    if output.shape != q.shape or output.stride(2) != 1:
+        raise ValueError("output must be [total_q, H, 128] with unit dim stride")
+    if q.dtype not in _DTYPE_ID or output.dtype not in _DTYPE_ID:
+        raise ValueError("q and output must be fp16, bf16 or fp32")
+    dev = pool.device
+    if q.device != dev or output.device != dev:
+        raise ValueError("q and output must be on the pool's device")
+    if seq_lens.dim() != 1 or total_q != seq_lens.numel() * decode_query_len:
+        raise ValueError("total_q must equal len(seq_lens) * decode_query_len")
+    if topk_idx.dim() != 3 or topk_idx.shape[:2] != (num_kv_heads, total_q):
+        raise ValueError("topk_idx must be [num_kv_heads, total_q, topk]")
+    tk = _i32(topk_idx, "topk_idx", dev)
+    if tk.stride(2) != 1:
+        tk = tk.contiguous()
+    sl = _i32(seq_lens, "seq_lens", dev).contiguous()
+    bt = _i32(block_table, "block_table", dev)
+    if bt.dim() != 2 or bt.size(0) != sl.numel() or bt.stride(1) != 1:
+        raise ValueError("block_table must be [num_reqs, max_blocks] with unit column stride")
+    max_topk = tk.size(2)
+    n_chunks = _chunks(total_q, num_kv_heads, max_topk)
+    lib = _lib.load()
+    need = int(lib.exl3_nvfp4_decode_workspace_size(total_q, Hq, n_chunks))
+    ws = workspace(dev, "q4_decode", need)
+    with torch.cuda.device(dev):
+        _lib.call("exl3_nvfp4_sparse_decode", q.data_ptr(), _DTYPE_ID[q.dtype], total_q, Hq,
+                  num_kv_heads, q.stride(0), q.stride(1), pool.data_ptr(), pool.size(0), tk.data_ptr(),
+                  tk.stride(0), tk.stride(1), max_topk, bt.data_ptr(), bt.stride(0), bt.size(1),
+                  sl.data_ptr(), int(decode_query_len), float(sm_scale), output.data_ptr(),
+                  _DTYPE_ID[output.dtype], output.stride(0), output.stride(1), n_chunks,
+                  ws.data_ptr(), ws.numel(), stream_of(dev))
