@@ -152,10 +152,8 @@ typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 template <int CB>
 __device__ __forceinline__ uint32_t hash32(uint32_t w) {
     if constexpr (CB == kCb3Inst) {
-        uint64_t r, carry;
-        asm("v_mad_u64_u32 %0, %1, %2, %3, %4"
-            : "=v"(r), "=s"(carry)
-            : "v"(w), "s"(89226354u), "v"((uint64_t)64248484u));
+        const uint64_t r = (uint64_t)w * 89226354u + 64248484u;
+        asm volatile("" ::"v"((uint32_t)(r >> 32)));  // keep the full product: one v_mad_u64_u32
         return (uint32_t)r;
     } else {
         return w * 0xCBAC1FEDu;
