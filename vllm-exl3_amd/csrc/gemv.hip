@@ -44,87 +44,121 @@ __device__ __forceinline__ half8_t dup4(uint32_t d0, uint32_t d1) {
 
 typedef __attribute__((address_space(1))) const v4u* gv4p;
 
-// Stream the wave's tile rows of one projection for the current chunk and
-// accumulate into acc[8] (one float4 per 16-column tile).
-//   tbase:     byte address of tile (first tile row of the chunk, j*8)
-//   row_bytes: bytes between consecutive tile rows (tiles_n * 32K)
-//   nkt:       tile rows in the chunk; the wave takes rows wave, wave+4, ...
-//   A:         this projection's activations [nkt][MRB][16] fp16 (kappa order)
-// The pipeline keeps kDepth rows in flight.  Its steady state has no
-// branches: lanes past the 256*K-byte row span reload the span's first 16
-// bytes, prefetches past the last row reload the last row (all in bounds),
-// and every lane stores into the 1 KB stage (bytes past the span are never
-// read).
-template <int K>
-struct RowStream {
-    const uint8_t* lane_base;  // this lane's 16 bytes of the wave's first row
-    size_t step;               // bytes between the wave's consecutive rows
-    int n;                     // rows of this wave in the chunk
-    v4u buf[kDepth];
+// Stream of one chunk's tile rows for one wave.  base: the wave's first row
+// (wave-uniform, so loads go through a scalar buffer resource and the row
+// advance is the scalar offset: no per-lane 64-bit pointers and no VALU
+// address arithmetic per row); step: bytes between the wave's consecutive
+// rows (4 tile rows); n: the wave's rows.  The lane's 16 bytes of a row are
+// LaneGeo::voff.
+struct Stream {
+    const uint8_t* base;
+    uint32_t step;
+    int n;
 };
 
-// Issue the loads of the wave's first kDepth rows (clamped, in bounds) so
-// they are in flight while the activations are staged.
-template <int K>
-__device__ __forceinline__ void stream_prefetch(RowStream<K>& rs, const uint8_t* tbase,
-                                                size_t row_bytes, int nkt, int wave, int lane) {
-    constexpr int span = 256 * K;
-    rs.n = nkt > wave ? (nkt - wave + kWaves - 1) / kWaves : 0;
-    rs.lane_base = tbase + (lane * 16 < span ? lane * 16 : 0) + (size_t)wave * row_bytes;
-    rs.step = row_bytes * kWaves;
-    if (rs.n == 0) return;
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d)
-        rs.buf[d] = __builtin_nontemporal_load((gv4p)(rs.lane_base + (size_t)min(d, rs.n - 1) * rs.step));
+// One 16-byte piece of a tile row: base + voff + soff, streamed (nt).
+__device__ __forceinline__ v4u load_row(const uint8_t* base, uint32_t voff, uint32_t soff) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7FFFFFFF, 0x00020000);
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 2));
 }
 
-// Consume the wave's rows: per row, stage 256*K bytes in LDS, refill the
-// pipeline, read the sixteen words this lane needs, decode and issue eight
-// MFMAs.  The steady state has no branches: lanes past the row span reload
-// its first 16 bytes, prefetches past the last row reload the last row (all
-// in bounds), and every lane stores into the 1 KB stage (bytes past the span
-// are never read).
-template <int K, int CB>
-__device__ __forceinline__ void stream_consume(RowStream<K>& rs, int wave, int lane, uint32_t* stage,
-                                               const uint16_t* A, int MRB, int arow,
-                                               float4_t (&acc)[8]) {
-    constexpr int tile_bytes = 32 * K;
-    const int n = rs.n;
-    if (n == 0) return;
-    const LaneWords lw = lane_words<K>(lane);
+// Consume one chunk of bit width K: per row, stage the 256*K bytes in LDS
+// (layout LK, see LaneGeo), refill the pipeline slot, read the sixteen words
+// this lane needs, decode and issue eight MFMAs.  buf[d] holds row d (mod
+// kDepth) on entry.  Refills of all but the last block of kDepth rows load
+// this chunk's later rows; the last block refills slot d with row d of the
+// next chunk (ns, lane offset ns_voff; the current chunk's first row again
+// when there is none), so the next chunk - another column block, split or
+// slot - starts with its pipeline already full.
+template <int CB, int LK>
+__device__ __forceinline__ void consume_chunk(v4u (&buf)[kDepth], const Stream& cs, const Stream& ns,
+                                              bool has_next, int ns_K, const LaneGeo& geo,
+                                              uint32_t ns_voff, int K_rt, int lane, int wave,
+                                              uint32_t* stage, const uint16_t* A, int MRB, int arow,
+                                              float4_t (&acc)[8]) {
+    const int K = LK ? LK : K_rt;
+    constexpr int ts = stage_tile_stride<LK>();
+    const int n = cs.n;
+    const uint32_t sh1 = (uint32_t)K, sh2 = 2u * K, sh3 = 3u * K;
     const int g = lane >> 4;
-    const uint8_t* st = reinterpret_cast<const uint8_t*>(stage);
+    uint8_t* st = reinterpret_cast<uint8_t*>(stage);
     const uint32_t* arow_p = reinterpret_cast<const uint32_t*>(A + (size_t)arow * 16 + 4 * g) +
                              (size_t)wave * MRB * 8;
     const int a_step = kWaves * MRB * 8;  // uint32 words between this wave's consecutive rows
-    auto consume = [&](int d, int i) {
-        reinterpret_cast<v4u*>(stage)[lane] = rs.buf[d];
-        rs.buf[d] = __builtin_nontemporal_load(
-            (gv4p)(rs.lane_base + (size_t)min(i + kDepth, n - 1) * rs.step));
+    auto put_g = [&](int d, const LaneGeo& gg) { *reinterpret_cast<v4u*>(st + gg.wr) = buf[d]; };
+    auto put = [&](int d) { put_g(d, geo); };
+    auto compute_g = [&](int i, const LaneGeo& gg) {
         const uint32_t* ap = arow_p + (size_t)i * a_step;
         // all sixteen words of the row first: one LDS latency per row
         uint32_t wh[8], wl[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            wh[t] = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_hi);
-            wl[t] = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_lo);
+            wh[t] = *reinterpret_cast<const uint32_t*>(st + t * ts + gg.off_hi);
+            wl[t] = *reinterpret_cast<const uint32_t*>(st + t * ts + gg.off_lo);
         }
         const half8_t a = dup4(ap[0], ap[1]);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             uint32_t b[4];
-            decode4<K, CB>(wh[t], wl[t], lw.shift, b);
+            decode4<CB>(wh[t], wl[t], gg.shift, sh3, sh2, sh1, b);
             acc[t] = mfma16x16x32(a, b, acc[t]);
         }
     };
-    int i = 0;
-    for (; i + kDepth <= n; i += kDepth) {
+    auto compute = [&](int i) { compute_g(i, geo); };
+    if (n % kDepth == 0 && ns.n >= kDepth) {
+        // whole blocks, branch-free; a block's refills target the rows of the
+        // next block, which for the last block (peeled) is the next chunk's
+        // first, at the next chunk's bit width.
+        auto block = [&](int i, const uint8_t* bb, uint32_t bs, int kk) {
+            // The lane offset is rebuilt from the lane id in every block (a
+            // few VALU): kept live across the loop it may be spilled, and the
+            // reload - a memory load like the trellis rows - would make every
+            // block wait for all rows in flight.
+            // (mixed-K launches rebuild all of the lane's geometry the same way)
+            uint32_t lid;
+            asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lid));
+            const uint32_t voff = (int)lid < 16 * kk ? lid * 16 : 0;
+            const LaneGeo gg = LK ? geo : lane_geo_padded(K, lid);
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d) consume(d, i + d);
+            for (int d = 0; d < kDepth; ++d) {
+                put_g(d, gg);
+                buf[d] = load_row(bb, voff, (uint32_t)d * bs);
+                compute_g(i + d, gg);
+                // keep each row's refill in its row: refills sunk past later
+                // rows leave those rows waiting for almost every load in flight
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        int i = 0;
+        for (; i + kDepth < n; i += kDepth) block(i, cs.base + (size_t)(i + kDepth) * cs.step, cs.step, K);
+        block(i, ns.base, ns.step, LK ? LK : ns_K);
+        return;
+    }
+    // short or ragged chunks (an input width that is not a multiple of 512):
+    // refills clamp to the chunk's last row, and the last block's rows past n
+    // only refill
+    const int last = (n - 1) & ~(kDepth - 1);  // first row of the last block
+    int i = 0;
+    for (; i < last; i += kDepth) {
+        const uint8_t* bb = cs.base + (size_t)i * cs.step;
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            put(d);
+            buf[d] = load_row(bb, geo.voff, (uint32_t)(min(i + d + kDepth, n - 1) - i) * cs.step);
+            compute(i + d);
+        }
     }
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d)
-        if (i + d < n) consume(d, i + d);
+    for (int d = 0; d < kDepth; ++d) {
+        if (i + d < n) {
+            put(d);
+            if (has_next) buf[d] = load_row(ns.base, ns_voff, (uint32_t)min(d, ns.n - 1) * ns.step);
+            compute(i + d);
+        } else if (has_next) {
+            buf[d] = load_row(ns.base, ns_voff, (uint32_t)min(d, ns.n - 1) * ns.step);
+        }
+    }
 }
 
 struct Proj {
@@ -310,8 +344,408 @@ __global__ __launch_bounds__(256) void act_rows_kernel(GemvParams p, int n_route
     dst[image_pos((int64_t)hb * 128 + lane + 64)] = half_to_bits(f32_to_f16_rne(a1));
 }
 
+// Copy the rotated activations of rows [row0, row0 + nr) for tile rows
+// [kt0, kt0 + nkt) from their image (row-major fp16 rows, MFMA k order inside
+// each 16 inputs) into the LDS operand layout A[kt][MRB][16].  Every load of
+// a batch is issued before its stores, so the copy costs about one L2 round
+// trip.
+__device__ __forceinline__ void stage_rows(const uint16_t* img, int64_t x_stride, int64_t row0, int nr,
+                                           int kt0, int nkt, int MRB, uint16_t* A, int tid) {
+    typedef __attribute__((address_space(1))) const v4u* gv4c;
+    const int pieces = nr * nkt * 2;  // 16-byte pieces, row-major
+    constexpr int kBatch = 4;  // loads in flight per thread: the restage runs beside the trellis pipeline
+    for (int b0 = 0; b0 < pieces; b0 += kThreads * kBatch) {
+        v4u v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int pc = b0 + b * kThreads + tid;
+            if (pc < pieces) {
+                const int h = pc & 1, kt = (pc >> 1) % nkt, r = (pc >> 1) / nkt;
+                v[b] = *(gv4c)(img + (row0 + r) * x_stride + (int64_t)(kt0 + kt) * 16 + 8 * h);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int pc = b0 + b * kThreads + tid;
+            if (pc < pieces) {
+                const int h = pc & 1, kt = (pc >> 1) % nkt, r = (pc >> 1) / nkt;
+                *reinterpret_cast<v4u*>(A + (kt * MRB + r) * 16 + 8 * h) = v[b];
+            }
+        }
+    }
+}
+
+// A workgroup's position in its sequence of chunks.  A unit is one (row
+// group, projection, split, 128-column block) - every unit streams the same
+// bytes, so equal unit ranges are equal work - numbered with the column
+// block fastest, then the split, the projection and the group, so
+// consecutive units of one group, projection and split share the staged
+// activations.  A row group is up to MRB rows of one slot; a chunk is one
+// staged range (up to C_hb 128-row blocks) of the split's input rows.
+struct Cursor {
+    int64_t u;  // unit; -1: past the workgroup's range
+    int grp, q, s, j, c;
+    // of (grp, q): slot, first row of the group within the slot, rows of the
+    // slot, its first activation / output row, bit width, trellis
+    int slot, rg, rows, row_base, K;
+    const uint8_t* trellis;
+};
+
+// Tables of the cursor's (group, projection); false when it has nothing to
+// stream (a batched expert id outside the table, a per-expert K outside
+// {2, 3, 4}).  Table selects are written out so that the kernel-argument
+// tables are never indexed with a run-time value.
+template <int MODE, int LK>
+__device__ __forceinline__ bool load_unit(const GemvParams& p, Cursor& c, int n_groups) {
+    if constexpr (MODE == kModeLinear) {
+        c.slot = 0;
+        c.rg = c.grp * p.MRB;
+        c.rows = p.m_rows;
+        c.row_base = 0;
+        c.trellis = reinterpret_cast<const uint8_t*>(p.w_trellis);
+        c.K = LK ? LK : p.kuni[0];
+        return true;
+    } else if constexpr (MODE == kModeBatched) {
+        const int gps = (p.batch_m + p.MRB - 1) / p.MRB;  // groups per slot
+        c.slot = c.grp / gps;
+        c.rg = (c.grp - c.slot * gps) * p.MRB;
+        c.rows = p.batch_m;
+        c.row_base = c.slot * p.batch_m;
+        c.K = LK ? LK : p.kuni[0];
+        const int e = p.expert_list[c.slot];
+        if (e < 0 || e >= p.n_ptr) return false;
+        c.trellis = reinterpret_cast<const uint8_t*>(p.tab[0][e]);
+        return true;
+    } else {
+        const int e = p.group_expert[c.grp];
+        c.slot = p.group_slot[c.grp];
+        c.rg = p.group_row0[c.grp];
+        if (c.grp >= n_groups) return false;
+        const bool up = MODE == kModeGateUp && (p.gateless || c.q);
+        const int64_t* tt = MODE == kModeDown ? p.tab[6] : up ? p.tab[3] : p.tab[0];
+        c.trellis = reinterpret_cast<const uint8_t*>(tt[e]);
+        c.rows = p.slot_rows[c.slot];
+        c.row_base = p.slot_start[c.slot];
+        if constexpr (LK != 0) {
+            c.K = LK;  // the host picks LK only for a uniform K
+            return c.rows > 0;
+        } else {
+            const int8_t* kt = MODE == kModeDown ? p.ktab[2] : up ? p.ktab[1] : p.ktab[0];
+            const int ku = MODE == kModeDown ? p.kuni[2] : up ? p.kuni[1] : p.kuni[0];
+            // the byte table is read with a vector load: make its value
+            // wave-uniform, or every address derived from it (the stream's
+            // buffer resource) would be treated as divergent
+            c.K = __builtin_amdgcn_readfirstlane(kt ? (int)kt[e] : ku);
+            // a per-expert K outside {2, 3, 4} streams nothing (never misaddresses)
+            return c.rows > 0 && c.K >= 2 && c.K <= 4;
+        }
+    }
+}
+
+// Step c to the next unit with something to stream; c.u = -1 past u1.  ok:
+// whether c's current (group, projection) has anything to stream.  Tables are
+// reloaded only when the group or projection changes.
+// (Units below u1 lie in groups below the group count: no check is needed.)
+template <int MODE, int LK>
+__device__ __forceinline__ void next_unit(const GemvParams& p, int64_t u1, int nq, int n_j, Cursor& c,
+                                          bool ok) {
+    c.c = 0;
+    do {
+        if (++c.u >= u1) {
+            c.u = -1;
+            return;
+        }
+        if (++c.j == n_j) {
+            c.j = 0;
+            if (++c.s == p.S) {
+                c.s = 0;
+                if (++c.q == nq) {
+                    c.q = 0;
+                    ++c.grp;
+                }
+                ok = load_unit<MODE, LK>(p, c, 0x7FFFFFFF);
+            }
+        }
+    } while (!ok);
+}
+
+// Place c at unit u (the first of the workgroup's range) or the next one with
+// something to stream.
+template <int MODE, int LK>
+__device__ __forceinline__ void seek_unit(const GemvParams& p, int64_t u, int64_t u1, int nq, int n_j,
+                                          int n_groups, Cursor& c) {
+    if (u >= u1) {
+        c.u = -1;
+        return;
+    }
+    const int per_group = nq * p.S * n_j;
+    c.grp = (int)(u / per_group);
+    int rem = (int)(u - (int64_t)c.grp * per_group);
+    c.j = rem % n_j;
+    rem /= n_j;
+    c.s = rem % p.S;
+    c.q = rem / p.S;
+    c.u = u;
+    c.c = 0;
+    if (!load_unit<MODE, LK>(p, c, n_groups)) next_unit<MODE, LK>(p, u1, nq, n_j, c, false);
+}
+
+// Step c to the next chunk of the workgroup's range.
+template <int MODE, int LK>
+__device__ __forceinline__ void advance(const GemvParams& p, int64_t u1, int nq, int n_j, int nc,
+                                        Cursor& c) {
+    if (++c.c < nc) return;
+    next_unit<MODE, LK>(p, u1, nq, n_j, c, true);
+}
+
+// The wave's trellis stream over chunk c (see Stream).
+__device__ __forceinline__ Stream stream_of(const GemvParams& p, const Cursor& c, int wave) {
+    const int tiles_n = p.out_features >> 4;
+    const size_t tile_bytes = 32u * (unsigned)c.K;
+    const size_t row_bytes = (size_t)tiles_n * tile_bytes;
+    const int hb0 = c.s * p.R_hb + c.c * p.C_hb;
+    const int nb = min(p.C_hb, p.R_hb - c.c * p.C_hb);
+    Stream st;
+    st.base = c.trellis + ((size_t)hb0 * 8 * tiles_n + (size_t)c.j * 8) * tile_bytes + (size_t)wave * row_bytes;
+    st.step = (uint32_t)(row_bytes * kWaves);
+    st.n = nb * 2;  // nb * 8 tile rows shared by the four waves
+    return st;
+}
+
+template <int MODE>
+__device__ __forceinline__ void stage_chunk(const GemvParams& p, const Cursor& c, uint16_t* A, int tid) {
+    const int hb0 = c.s * p.R_hb + c.c * p.C_hb;
+    const int nb = min(p.C_hb, p.R_hb - c.c * p.C_hb);
+    const uint16_t* img = reinterpret_cast<const uint16_t*>((MODE == kModeGateUp && c.q) ? p.x2 : p.x);
+    stage_rows(img, p.x_stride, (int64_t)c.row_base + c.rg, min(p.MRB, c.rows - c.rg), hb0 * 8, nb * 8,
+               p.MRB, A, tid);
+}
+
+// Sum of the four waves' partials at (row, column), in wave order.
+__device__ __forceinline__ float red_sum(const float* red, int MRB, int row, int c) {
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v += red[(w * MRB + row) * 128 + c];
+    return v;
+}
+
+// Persistent decode GEMV.  The grid is at most one wave of resident
+// workgroups; workgroup b takes units [b*U/G, (b+1)*U/G) of the U units of
+// the launch (U from the device-side slot count for the MoE phases) and
+// streams their chunks back to back: the trellis pipeline runs across chunk
+// and unit boundaries, activations are restaged only when the slot,
+// projection, split, row group or input range changes, and each finished
+// (unit, row group) is reduced over the waves in LDS and written as a raw
+// split partial (or, for a single split of a plain or batched linear,
+// finished in place).
+template <int CB, int MODE, int LK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemv_kernel(GemvParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar stream bases
+    const int n_j = p.out_features >> 7;
+    const int nq = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
+    const int nc = (p.R_hb + p.C_hb - 1) / p.C_hb;
+    const int MRB = p.MRB;
+    int n_groups;
+    if constexpr (MODE == kModeLinear || MODE == kModeBatched) {
+        n_groups = p.max_groups;  // ceil(m / MRB) (per listed expert)
+    } else {
+        n_groups = min(*p.n_groups, p.max_groups);
+    }
+    const int64_t U = (int64_t)n_groups * nq * p.S * n_j;
+    const int64_t u0 = (int64_t)blockIdx.x * U / gridDim.x;
+    const int64_t u1 = (int64_t)(blockIdx.x + 1) * U / gridDim.x;
+
+    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16][red: 4 waves x MRB x 128 fp32]
+    uint32_t* stage = reinterpret_cast<uint32_t*>(lds) + wave * (kStageBytes / 4);
+    uint16_t* A = reinterpret_cast<uint16_t*>(lds + kWaves * kStageBytes);
+    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes + (size_t)p.C_hb * 8 * MRB * 32);
+
+    if constexpr (MODE == kModeBatched) {
+        // ids outside the table give zero outputs (written by the finisher when split)
+        if (p.S == 1) {
+            const int per_group = p.S * n_j, gps = (p.batch_m + MRB - 1) / MRB;
+            for (int64_t u = u0; u < u1; ++u) {
+                const int grp = (int)(u / per_group), j = (int)(u % n_j);
+                const int slot = grp / gps, rg = (grp - slot * gps) * MRB;
+                const int e = p.expert_list[slot];
+                if (e >= 0 && e < p.n_ptr) continue;
+                const int nr = min(MRB, p.batch_m - rg);
+                for (int i = tid; i < nr * 128; i += kThreads)
+                    store_out(p.out, p.out_dtype,
+                              (int64_t)(slot * p.batch_m + rg + (i >> 7)) * p.out_stride + j * 128 + (i & 127),
+                              0.0f);
+            }
+        }
+    }
+    Cursor cur;
+    seek_unit<MODE, LK>(p, u0, u1, nq, n_j, n_groups, cur);
+    if (cur.u < 0) return;
+
+    v4u buf[kDepth];
+    LaneGeo geo = lane_geo<LK>(cur.K, lane);
+    Stream cs = stream_of(p, cur, wave);
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) buf[d] = load_row(cs.base, geo.voff, (uint32_t)min(d, cs.n - 1) * cs.step);
+    Cursor nxt = cur;
+    advance<MODE, LK>(p, u1, nq, n_j, nc, nxt);
+    stage_chunk<MODE>(p, cur, A, tid);
+    __syncthreads();
+
+    float4_t acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int g = lane >> 4;
+    const int col_nu = sigma_col(lane & 15);
+    while (true) {
+        const bool has_next = nxt.u >= 0;
+        const bool same_k = !has_next || nxt.K == cur.K;
+        // with no next chunk the last refills re-read the current one's first row
+        const Stream ns = has_next ? stream_of(p, nxt, wave) : Stream{cs.base, 0u, cs.n};
+        const uint32_t ns_voff = same_k ? geo.voff : (lane < 16 * nxt.K ? lane * 16 : 0);
+        const int nr = min(MRB, cur.rows - cur.rg);
+        const int arow = min(lane & 15, nr - 1);
+        consume_chunk<CB, LK>(buf, cs, ns, has_next, has_next ? nxt.K : cur.K, geo, ns_voff, cur.K, lane, wave,
+                              stage, A, MRB, arow, acc);
+        const bool flush = !has_next || nxt.u != cur.u;
+        const bool restage =
+            has_next && (nxt.grp != cur.grp || nxt.q != cur.q || nxt.s != cur.s || nxt.c != cur.c);
+        if (flush) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 4 * g + i;
+                    if (row < nr) red[(wave * MRB + row) * 128 + t * 16 + col_nu] = acc[t][i];
+                }
+                acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        if (flush || restage) __syncthreads();
+        if (restage) stage_chunk<MODE>(p, nxt, A, tid);
+        if (flush) {
+            if ((MODE == kModeLinear || MODE == kModeBatched) && p.S == 1) {
+                // single split: finish in place
+                const uint16_t* svh = p.w_svh;
+                if constexpr (MODE == kModeBatched)
+                    svh = reinterpret_cast<const uint16_t*>(p.tab[2][p.expert_list[cur.slot]]);
+                for (int r = wave; r < nr; r += kWaves) {
+                    float v0 = red_sum(red, MRB, r, lane), v1 = red_sum(red, MRB, r, lane + 64);
+                    finish_block(v0, v1, svh, cur.j * 128 + lane, lane);
+                    const int64_t o = (int64_t)(cur.row_base + cur.rg + r) * p.out_stride + cur.j * 128 + lane;
+                    store_out(p.out, p.out_dtype, o, v0);
+                    store_out(p.out, p.out_dtype, o + 64, v1);
+                }
+            } else {
+                float* dst = p.ws + (((int64_t)cur.q * p.S + cur.s) * p.n_rows_ws + cur.row_base + cur.rg) *
+                                        p.out_features +
+                             cur.j * 128;
+                for (int e = tid; e < nr * 128; e += kThreads)
+                    dst[(int64_t)(e >> 7) * p.out_features + (e & 127)] = red_sum(red, MRB, e >> 7, e & 127);
+            }
+        }
+        if (!has_next) break;
+        if (flush || restage) __syncthreads();
+        cur = nxt;
+        cs = ns;
+        advance<MODE, LK>(p, u1, nq, n_j, nc, nxt);
+        if (!same_k) geo = lane_geo<LK>(cur.K, lane);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One-unit-per-workgroup GEMV, for launches whose units fill at most about two
+// rounds of resident workgroups (decode at small batch): workgroup = (slot,
+// projection, split, 128-column block), all row groups of the slot in turn.
+// Each workgroup starts its trellis stream cold, but the launch needs no unit
+// count and no group tables, and keeps the fewest registers live.
+// ---------------------------------------------------------------------------
+// Stream the wave's tile rows of one projection for the current chunk and
+// accumulate into acc[8] (one float4 per 16-column tile).
+//   tbase:     byte address of tile (first tile row of the chunk, j*8)
+//   row_bytes: bytes between consecutive tile rows (tiles_n * 32K)
+//   nkt:       tile rows in the chunk; the wave takes rows wave, wave+4, ...
+//   A:         this projection's activations [nkt][MRB][16] fp16 (kappa order)
+// The pipeline keeps kDepth rows in flight.  Its steady state has no
+// branches: lanes past the 256*K-byte row span reload the span's first 16
+// bytes, prefetches past the last row reload the last row (all in bounds),
+// and every lane stores into the 1 KB stage (bytes past the span are never
+// read).
+template <int K>
+struct WgStream {
+    const uint8_t* base;  // the wave's first row (wave-uniform: a scalar buffer resource)
+    uint32_t voff;        // this lane's 16 bytes of a row
+    uint32_t step;        // bytes between the wave's consecutive rows (the scalar offset)
+    int n;                // rows of this wave in the chunk
+    v4u buf[kDepth];
+};
+
+// Issue the loads of the wave's first kDepth rows (clamped, in bounds) so
+// they are in flight while the activations are staged.
+template <int K>
+__device__ __forceinline__ void wg_prefetch(WgStream<K>& rs, const uint8_t* tbase,
+                                                size_t row_bytes, int nkt, int wave, int lane) {
+    constexpr int span = 256 * K;
+    rs.n = nkt > wave ? (nkt - wave + kWaves - 1) / kWaves : 0;
+    rs.base = tbase + (size_t)wave * row_bytes;
+    rs.voff = lane * 16 < span ? lane * 16 : 0;
+    rs.step = (uint32_t)(row_bytes * kWaves);  // a chunk lies within one projection (< 2 GiB)
+    if (rs.n == 0) return;
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) rs.buf[d] = load_row(rs.base, rs.voff, (uint32_t)min(d, rs.n - 1) * rs.step);
+}
+
+// Consume the wave's rows: per row, stage 256*K bytes in LDS, refill the
+// pipeline, read the sixteen words this lane needs, decode and issue eight
+// MFMAs.  The steady state has no branches: lanes past the row span reload
+// its first 16 bytes, prefetches past the last row reload the last row (all
+// in bounds), and every lane stores into the 1 KB stage (bytes past the span
+// are never read).
+template <int K, int CB>
+__device__ __forceinline__ void wg_consume(WgStream<K>& rs, int wave, int lane, uint32_t* stage,
+                                               const uint16_t* A, int MRB, int arow,
+                                               float4_t (&acc)[8]) {
+    constexpr int tile_bytes = 32 * K;
+    const int n = rs.n;
+    if (n == 0) return;
+    const LaneGeo lw = lane_geo<K>(K, lane);
+    const int g = lane >> 4;
+    const uint8_t* st = reinterpret_cast<const uint8_t*>(stage);
+    const uint32_t* arow_p = reinterpret_cast<const uint32_t*>(A + (size_t)arow * 16 + 4 * g) +
+                             (size_t)wave * MRB * 8;
+    const int a_step = kWaves * MRB * 8;  // uint32 words between this wave's consecutive rows
+    auto consume = [&](int d, int i) {
+        reinterpret_cast<v4u*>(stage)[lane] = rs.buf[d];
+        rs.buf[d] = load_row(rs.base, rs.voff, (uint32_t)min(i + kDepth, n - 1) * rs.step);
+        const uint32_t* ap = arow_p + (size_t)i * a_step;
+        // all sixteen words of the row first: one LDS latency per row
+        uint32_t wh[8], wl[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            wh[t] = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_hi);
+            wl[t] = *reinterpret_cast<const uint32_t*>(st + t * tile_bytes + lw.off_lo);
+        }
+        const half8_t a = dup4(ap[0], ap[1]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t b[4];
+            decode4<CB>(wh[t], wl[t], lw.shift, 3 * K, 2 * K, K, b);
+            acc[t] = mfma16x16x32(a, b, acc[t]);
+        }
+    };
+    int i = 0;
+    for (; i + kDepth <= n; i += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) consume(d, i + d);
+    }
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d)
+        if (i + d < n) consume(d, i + d);
+}
+
 // Everything one projection of one row group needs, shared by all waves.
-struct RowGroup {
+struct WgGroup {
     int rg, nr, arow, row_base, hb_first, j, tiles_n, expert;
     const void* img;  // rotated activation rows of the streamed projection
 };
@@ -320,7 +754,7 @@ struct RowGroup {
 // from their image (row-major fp16 rows, MFMA k order inside each 16 inputs)
 // into the LDS operand layout A[kt][MRB][16].  Every load of a batch is
 // issued before its stores, so the copy costs about one L2 round trip.
-__device__ __forceinline__ void stage_rows(const GemvParams& p, const RowGroup& G, int kt0, int nkt,
+__device__ __forceinline__ void wg_stage_rows(const GemvParams& p, const WgGroup& G, int kt0, int nkt,
                                            uint16_t* A, int tid) {
     typedef __attribute__((address_space(1))) const v4u* gv4c;
     const int MRB = p.MRB;
@@ -353,7 +787,7 @@ __device__ __forceinline__ void stage_rows(const GemvParams& p, const RowGroup& 
 // 128-row blocks, stream its tiles, and leave each wave's partial sums in
 // red[wave][row][128].  acc lives only inside this K-specialised routine.
 template <int K, int CB>
-__device__ __forceinline__ void run_projection(const GemvParams& p, const RowGroup& G, const Proj& pq,
+__device__ __forceinline__ void wg_projection(const GemvParams& p, const WgGroup& G, const Proj& pq,
                                                uint32_t* stage, uint16_t* A, float* red, bool restage,
                                                int wave, int lane) {
     float4_t acc[8];
@@ -365,19 +799,19 @@ __device__ __forceinline__ void run_projection(const GemvParams& p, const RowGro
     for (int c0 = 0; c0 < p.R_hb; c0 += p.C_hb) {
         const int nb = min(p.C_hb, p.R_hb - c0);
         // trellis bytes of this chunk start moving before the staging below
-        RowStream<K> rs;
+        WgStream<K> rs;
         const uint8_t* tb = pq.trellis +
                             ((size_t)(G.hb_first + c0) * 8 * G.tiles_n + (size_t)G.j * 8) * tile_bytes;
-        stream_prefetch<K>(rs, tb, row_bytes, nb * 8, wave, lane);
+        wg_prefetch<K>(rs, tb, row_bytes, nb * 8, wave, lane);
         if (restage) {
             __syncthreads();
-            stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
+            wg_stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
             __syncthreads();
         }
-        stream_consume<K, CB>(rs, wave, lane, stage, A, MRB, G.arow, acc);
+        wg_consume<K, CB>(rs, wave, lane, stage, A, MRB, G.arow, acc);
     }
     // when red overlays A, every wave must be done reading A first
-    if (p.NJ == 1) __syncthreads();
+    __syncthreads();
     const int g = lane >> 4;
     const int col_nu = sigma_col(lane & 15);
 #pragma unroll
@@ -390,26 +824,19 @@ __device__ __forceinline__ void run_projection(const GemvParams& p, const RowGro
     __syncthreads();
 }
 
-// Sum of the four waves' partials at (row, column), in wave order.
-__device__ __forceinline__ float red_sum(const float* red, int MRB, int row, int c) {
-    float v = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) v += red[(w * MRB + row) * 128 + c];
-    return v;
-}
-
 template <int CB, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemv_wg_kernel(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nJB = (p.out_features >> 7) / p.NJ;  // blocks of NJ 128-column blocks
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar stream bases
+    const int nJB = p.out_features >> 7;
     // gate/up: each workgroup streams one of the two projections
     const int nsplit_proj = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
     const int item = blockIdx.x;
     const int qsel = item % nsplit_proj;
     const int s = (item / nsplit_proj) % p.S;
     const int rest = item / nsplit_proj / p.S;
-    RowGroup G;
+    WgGroup G;
     const int jb = rest % nJB;
     const int slot = rest / nJB;
 
@@ -426,11 +853,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         if (G.expert < 0 || G.expert >= p.n_ptr) {
             // not a table entry: zero outputs (written by the finisher when split)
             if (p.S == 1)
-                for (int e = tid; e < rows * 128 * p.NJ; e += kThreads)
+                for (int e = tid; e < rows * 128; e += kThreads)
                     store_out(p.out, p.out_dtype,
-                              (int64_t)(G.row_base + (e >> 7) % rows) * p.out_stride +
-                                  (jb * p.NJ + (e >> 7) / rows) * 128 + (e & 127),
-                              0.0f);
+                              (int64_t)(G.row_base + (e >> 7)) * p.out_stride + jb * 128 + (e & 127), 0.0f);
             return;
         }
     } else {
@@ -462,25 +887,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     G.img = (MODE == kModeGateUp && qsel) ? p.x2 : p.x;
     G.tiles_n = p.out_features >> 4;
     G.hb_first = s * p.R_hb;  // first 128-row input block of this split
-    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16][red: 4 waves x MRB x
-    // 128 fp32].  With one column block per workgroup red overlays A; with
-    // NJ > 1 (single-chunk phases only) A is staged once per row group and
-    // kept for every column block.
+    // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16 | red: 4 waves x MRB
+    // x 128 fp32] (red overlays A: the column block's reduction follows its
+    // last read of A)
     uint32_t* stage = reinterpret_cast<uint32_t*>(lds) + wave * (kStageBytes / 4);
     uint16_t* A = reinterpret_cast<uint16_t*>(lds + kWaves * kStageBytes);
-    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes +
-                                          (p.NJ > 1 ? (size_t)p.C_hb * 8 * MRB * 32 : 0));
+    float* red = reinterpret_cast<float*>(lds + kWaves * kStageBytes);
 
     for (G.rg = 0; G.rg < rows; G.rg += MRB) {
       G.nr = min(MRB, rows - G.rg);
       G.arow = min(lane & 15, G.nr - 1);
-      for (int jj = 0; jj < p.NJ; ++jj) {
-        G.j = jb * p.NJ + jj;
-        const bool restage = jj == 0;
+      {
+        G.j = jb;
+        const bool restage = true;
         switch (pr.K) {
-            case 2: run_projection<2, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
-            case 3: run_projection<3, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
-            case 4: run_projection<4, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
+            case 2: wg_projection<2, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
+            case 3: wg_projection<3, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
+            case 4: wg_projection<4, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
             default: break;  // rejected on the host
         }
         if ((MODE == kModeLinear || MODE == kModeBatched) && p.S == 1) {
@@ -541,17 +964,19 @@ __global__ __launch_bounds__(256) void linear_finish_kernel(const float* __restr
 // ---------------------------------------------------------------------------
 // Routing for layers with more than kRouteMaxLocal local experts: bitonic
 // sort of the T*topk routes by local expert id (sentinel routes last) in one
-// workgroup, then slots = runs of one expert.  Same outputs as the multisplit
-// router of route.hip (which handles every layer up to kRouteMaxLocal
-// experts); at most kMaxRoutes routes.
+// workgroup, then slots = runs of one expert and, for tile_rows > 0, each
+// slot's row tiles of tile_rows rows.  Same outputs as the multisplit router
+// of route.hip (which handles every layer up to kRouteMaxLocal experts); at
+// most kMaxRoutes routes.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kRouteThreads) void route_bitonic_kernel(const void* ids, int ids_i64,
                                                                      int n_routes, int topk,
                                                                      int n_local,
                                                                      const int32_t* n_valid,
-                                                                     RouteOut o) {
+                                                                     int tile_rows, RouteOut o) {
     __shared__ uint32_t key[kMaxRoutes];
     __shared__ int wave_sum[kRouteThreads / 64];
+    __shared__ int wave_tiles[kRouteThreads / 64];
     const int tid = threadIdx.x;
     int np2 = 1;
     while (np2 < n_routes) np2 <<= 1;
@@ -591,30 +1016,50 @@ __global__ __launch_bounds__(kRouteThreads) void route_bitonic_kernel(const void
     // a contiguous range of sorted positions
     const int per = (n_routes + kRouteThreads - 1) / kRouteThreads;
     const int p0 = tid * per, p1 = min(n_routes, p0 + per);
-    int cnt = 0;
+    // slots (runs) starting in this thread's range, and their row tiles
+    auto run_end = [&](int q, uint32_t e) {
+        int end = q + 1;
+        while (end < n_routes && (key[end] >> kRouteBits) == e) ++end;
+        return end;
+    };
+    int cnt = 0, tcnt = 0;
     for (int q = p0; q < p1; ++q) {
         const uint32_t e = key[q] >> kRouteBits;
-        if (e < (uint32_t)n_local && (q == 0 || (key[q - 1] >> kRouteBits) != e)) ++cnt;
+        if (e < (uint32_t)n_local && (q == 0 || (key[q - 1] >> kRouteBits) != e)) {
+            ++cnt;
+            if (tile_rows > 0) tcnt += (run_end(q, e) - q + tile_rows - 1) / tile_rows;
+        }
     }
     const int lane = tid & 63, w = tid >> 6;
-    int incl = cnt;
+    int incl = cnt, tincl = tcnt;
     for (int d = 1; d < 64; d <<= 1) {
         const int t = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += t;
+        const int tt = __shfl_up(tincl, d, 64);
+        if (lane >= d) {
+            incl += t;
+            tincl += tt;
+        }
     }
-    if (lane == 63) wave_sum[w] = incl;
+    if (lane == 63) {
+        wave_sum[w] = incl;
+        wave_tiles[w] = tincl;
+    }
     __syncthreads();
     if (tid == 0) {
-        int acc = 0;
+        int acc = 0, tacc = 0;
         for (int i = 0; i < kRouteThreads / 64; ++i) {
-            const int t = wave_sum[i];
+            const int t = wave_sum[i], tt = wave_tiles[i];
             wave_sum[i] = acc;
+            wave_tiles[i] = tacc;
             acc += t;
+            tacc += tt;
         }
         o.n_active[0] = acc;
+        if (tile_rows > 0) o.n_mtiles[0] = tacc;
     }
     __syncthreads();
-    int slot = wave_sum[w] + incl - cnt;  // exclusive prefix for this thread's range
+    int slot = wave_sum[w] + incl - cnt;      // exclusive prefixes for this thread's range
+    int tile = wave_tiles[w] + tincl - tcnt;
     for (int q = p0; q < p1; ++q) {
         const uint32_t kq = key[q];
         const uint32_t e = kq >> kRouteBits;
@@ -626,9 +1071,14 @@ __global__ __launch_bounds__(kRouteThreads) void route_bitonic_kernel(const void
             if (q == 0 || (key[q - 1] >> kRouteBits) != e) {
                 o.slot_expert[slot] = (int)e;
                 o.slot_start[slot] = q;
-                int end = q + 1;
-                while (end < n_routes && (key[end] >> kRouteBits) == e) ++end;
-                o.slot_rows[slot] = end - q;
+                const int rows = run_end(q, e) - q;
+                o.slot_rows[slot] = rows;
+                if (tile_rows > 0)
+                    for (int k = 0; k * tile_rows < rows; ++k, ++tile) {
+                        o.mt_slot[tile] = slot;
+                        if (o.mt_expert) o.mt_expert[tile] = (int)e;
+                        o.mt_row0[tile] = k * tile_rows;
+                    }
                 ++slot;
             }
         } else {
@@ -688,18 +1138,19 @@ __global__ __launch_bounds__(kCombineWaves * 64) void combine_kernel(
 // Host-side planning (shared by the workspace queries and the launches)
 // ---------------------------------------------------------------------------
 constexpr int kMaxSplits = 16;
-// Column blocks per workgroup: the planner supports NJ > 1 (activations
-// staged once per row group), but on MI355X it measured slower than more,
-// shorter workgroups (each block's first rows wait on HBM again), so it is
-// capped at 1.
-constexpr int kMaxNJ = 1;
 // Launch cost model (microseconds, measured on MI355X under a full decode
-// load): a workgroup's fixed latency (argument, slot, table and activation
-// loads before its first tile row) and a wave's time per tile row with three
-// workgroups per CU (decode-VALU bound), plus the consumer's cost per split.
+// load): a workgroup's fixed latency before its first tile row (argument,
+// group, table and activation loads, cold trellis stream), a wave's time per
+// tile row with three workgroups per CU, the cost of one unit's wave
+// reduction and partial write, of one activation restage, and the
+// consumer's cost per split.
 constexpr double kWgFixedUs = 8.0;
-constexpr double kRowUs = 0.6;
+constexpr double kRowUs = 0.9;
+constexpr double kUnitUs = 2.0;
+constexpr double kStageUs = 1.0;
 constexpr double kSplitUs = 0.15;
+// LDS per workgroup that keeps three workgroups resident on a 160 KB CU.
+constexpr size_t kLdsBudget = 53 * 1024;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -717,59 +1168,113 @@ inline int resident_workgroups() {
     return n;
 }
 
-// Hadamard blocks whose activations fit the LDS budget at once.
-inline int pick_chunk(int R_hb, int nproj, int MRB) {
-    (void)nproj;
-    const int per_hb = 8 * MRB * 16 * 2;  // bytes of staged activations per 128-row block
+inline size_t gemv_red_bytes(int MRB) { return (size_t)kWaves * MRB * 128 * 4; }
+
+// Hadamard blocks whose activations are staged at once: what the LDS budget
+// leaves after the stage slots and the reduction buffer.  For a split of a
+// multiple of 4 blocks the chunk is a multiple of 4 dividing it, so every
+// chunk gives each wave a whole number of kDepth-row blocks.
+inline int pick_chunk(int R_hb, int MRB) {
+    const size_t fixed = kWaves * kStageBytes + gemv_red_bytes(MRB);
+    const size_t per_hb = (size_t)8 * MRB * 16 * 2;  // staged activations per 128-row block
+    int cmax = fixed < kLdsBudget ? (int)((kLdsBudget - fixed) / per_hb) : 1;
+    if (cmax < 1) cmax = 1;
+    if (R_hb % 4 == 0 && cmax >= 4) {
+        for (int c = cmax - cmax % 4; c >= 4; c -= 4)
+            if (R_hb % c == 0) return c;
+    }
+    return cmax < R_hb ? cmax : R_hb;
+}
+
+inline size_t gemv_lds_bytes(int C_hb, int MRB) {
+    return kWaves * kStageBytes + (size_t)C_hb * 8 * MRB * 16 * 2 + gemv_red_bytes(MRB);
+}
+
+struct PhasePlan {
+    int S, R_hb, C_hb, grid;
+    int wg;  // 1: one unit per workgroup (gemv_wg_kernel); 0: persistent (gemv_kernel)
+    size_t lds;
+};
+
+// One-unit-per-workgroup plan: activation chunk within a 40 KB budget (the
+// reduction buffer overlays it), cost = rounds of resident workgroups x
+// (fixed latency + rows x row time) + the consumer's per-split cost.
+constexpr double kWgRowUs = 0.6;  // a wave's time per tile row, cold-started workgroups
+constexpr int kMinUnitsPerWg = 6;
+
+inline int pick_chunk_wg(int R_hb, int MRB) {
+    const int per_hb = 8 * MRB * 16 * 2;
     int c = (40 * 1024) / per_hb;
     if (c < 1) c = 1;
     return c < R_hb ? c : R_hb;
 }
 
-inline size_t gemv_lds_bytes(int C_hb, int NJ, int MRB) {
-    const size_t a = (size_t)C_hb * 8 * MRB * 16 * 2;
-    const size_t r = (size_t)kWaves * MRB * 128 * 4;
-    return kWaves * kStageBytes + (NJ > 1 ? a + r : (a > r ? a : r));
-}
-
-struct PhasePlan {
-    int S, R_hb, C_hb, NJ;
-    size_t lds;
-};
-
-// Split count S (a divisor of the input's 128-blocks) and column blocks per
-// workgroup NJ (a divisor of the output's 128-blocks; above 1 only when a
-// split's activations are staged in one chunk) minimising the modelled time:
-// rounds of resident workgroups x (fixed latency + NJ x rows per wave x row
-// time), plus the consumer's per-split cost.  base_items = slots x streamed
-// projections.
-inline PhasePlan plan_phase(int in_f, int out_f, int base_items, int MRB) {
+inline PhasePlan plan_phase_wg(int in_f, int out_f, int wg_items, int MRB) {
     const int n_hb = in_f / 128, n_j = out_f / 128;
     const int cap = resident_workgroups();
-    PhasePlan best = {1, n_hb, pick_chunk(n_hb, 1, MRB), 1, 0};
+    PhasePlan best = {1, n_hb, pick_chunk_wg(n_hb, MRB), 1, 1, 0};
     double best_t = 1e30;
     for (int S = 1; S <= kMaxSplits && S <= n_hb; ++S) {
         if (n_hb % S) continue;
         const int R_hb = n_hb / S;
-        const int C_hb = pick_chunk(R_hb, 1, MRB);
-        for (int NJ = 1; NJ <= kMaxNJ && NJ <= n_j; ++NJ) {
-            if (n_j % NJ || (NJ > 1 && C_hb < R_hb)) continue;
-            const int64_t items = (int64_t)base_items * (n_j / NJ) * S;
-            const int64_t rounds = (items + cap - 1) / cap;
-            const double rows = R_hb * 8.0 / kWaves;
-            const double t = rounds * (kWgFixedUs + NJ * rows * kRowUs) + S * kSplitUs;
-            if (t < best_t) {
-                best_t = t;
-                best = {S, R_hb, C_hb, NJ, 0};
-            }
+        const int64_t items = (int64_t)wg_items * n_j * S;
+        const int64_t rounds = (items + cap - 1) / cap;
+        const double t = rounds * (kWgFixedUs + R_hb * 8.0 / kWaves * kWgRowUs) + S * kSplitUs;
+        if (t < best_t) {
+            best_t = t;
+            best = {S, R_hb, pick_chunk_wg(R_hb, MRB), (int)items, 1, 0};
         }
     }
-    best.lds = gemv_lds_bytes(best.C_hb, best.NJ, MRB);
+    const size_t a = (size_t)best.C_hb * 8 * MRB * 16 * 2, r = gemv_red_bytes(MRB);
+    best.lds = kWaves * kStageBytes + (a > r ? a : r);
+    return best;
+}
+
+// Split count S (a divisor of the input's 128-blocks; for an input of a
+// multiple of 4 blocks, one leaving a multiple of 4 per split, so that every
+// chunk streams whole kDepth-row blocks) of the persistent launch minimising
+// the modelled time: one fixed latency, then the most loaded workgroup's
+// units (ceil(units / resident)) at rows x row time plus the unit's
+// reduction and restages, plus the consumer's per-split cost.  Items are row
+// groups x streamed projections: est_items the expected count, max_items
+// the bound the grid is sized for (they differ for the MoE phases).  The
+// persistent kernel pays off once a workgroup holds many units (it balances
+// the load and keeps the pipeline warm across them; a unit switch still
+// costs about a memory round trip); below kMinUnitsPerWg the
+// one-unit-per-workgroup plan (wg_items = slots x streamed projections) is
+// used.
+inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, int wg_items, int MRB) {
+    const int n_hb = in_f / 128, n_j = out_f / 128;
+    const int cap = resident_workgroups();
+    PhasePlan best = {1, n_hb, pick_chunk(n_hb, MRB), 1, 0, 0};
+    double best_t = 1e30;
+    int64_t best_per_wg = 0;
+    for (int S = 1; S <= kMaxSplits && S <= n_hb; ++S) {
+        if (n_hb % S) continue;
+        const int R_hb = n_hb / S;
+        if (n_hb % 4 == 0 && R_hb % 4 != 0) continue;
+        const int C_hb = pick_chunk(R_hb, MRB);
+        const int nc = (R_hb + C_hb - 1) / C_hb;
+        const int64_t units = (int64_t)est_items * n_j * S;
+        const int64_t units_max = (int64_t)max_items * n_j * S;
+        const int grid = (int)(units_max < cap ? units_max : cap);
+        const int64_t per_wg = (units + grid - 1) / grid;
+        const double t = kWgFixedUs +
+                         per_wg * (R_hb * 8.0 / kWaves * kRowUs + kUnitUs + (nc > 1 ? nc * kStageUs : 0.0)) +
+                         S * kSplitUs;
+        if (t < best_t) {
+            best_t = t;
+            best_per_wg = per_wg;
+            best = {S, R_hb, C_hb, grid, 0, 0};
+        }
+    }
+    if (best_per_wg < kMinUnitsPerWg) return plan_phase_wg(in_f, out_f, wg_items, MRB);
+    best.lds = gemv_lds_bytes(best.C_hb, MRB);
     return best;
 }
 
 struct MoePlan {
-    int n_routes, max_slots, MRB, nproj;
+    int n_routes, max_slots, max_groups, MRB, nproj;
     PhasePlan gu, dn;
     size_t off_route, off_wsgu, off_wsd, off_img, off_imgd, total;
 };
@@ -783,11 +1288,22 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
     // slots run extra row groups (the weights are streamed once per group)
     m.MRB = (int)(T < kMoeMRB ? (T < 1 ? 1 : T) : kMoeMRB);
     m.nproj = gateless ? 1 : 2;
-    m.gu = plan_phase((int)hidden, (int)inter, m.max_slots * m.nproj, m.MRB);
-    m.dn = plan_phase((int)inter, (int)hidden, m.max_slots, m.MRB);
+    // row groups: sum over slots of ceil(rows / MRB) <= routes, and
+    // <= (routes + slots * (MRB - 1)) / MRB
+    {
+        const int64_t a = m.n_routes, b = (m.n_routes + (int64_t)m.max_slots * (m.MRB - 1)) / m.MRB;
+        m.max_groups = (int)(a < b ? a : b);
+    }
+    // the planner's work estimate: about one group per routed slot at decode
+    const int64_t est = m.n_routes / m.MRB > m.max_slots ? m.n_routes / m.MRB : m.max_slots;
+    const int est_groups = (int)(est < m.max_groups ? est : m.max_groups);
+    m.gu = plan_phase((int)hidden, (int)inter, est_groups * m.nproj, m.max_groups * m.nproj,
+                      m.max_slots * m.nproj, m.MRB);
+    m.dn = plan_phase((int)inter, (int)hidden, est_groups, m.max_groups, m.max_slots, m.MRB);
     size_t off = 0;
     m.off_route = off;
-    off += align256(sizeof(int) * (1 + 3 * (size_t)m.max_slots + 3 * (size_t)m.n_routes));
+    off += align256(sizeof(int) * (2 + 3 * (size_t)m.max_slots + 3 * (size_t)m.n_routes +
+                                   3 * (size_t)m.max_groups));
     m.off_wsgu = off;
     off += align256(4 * (size_t)m.nproj * m.gu.S * m.n_routes * inter);
     m.off_wsd = off;
@@ -809,7 +1325,8 @@ struct LinPlan {
 inline LinPlan plan_linear(int64_t m, int64_t in_f, int64_t out_f) {
     LinPlan lp;
     lp.MRB = (int)(m < kMaxMRB ? m : kMaxMRB);
-    lp.ph = plan_phase((int)in_f, (int)out_f, 1, lp.MRB);
+    const int groups = (int)((m + lp.MRB - 1) / lp.MRB);
+    lp.ph = plan_phase((int)in_f, (int)out_f, groups, groups, 1, lp.MRB);
     // [split partials (S > 1)][rotated input rows, fp16]
     lp.off_img = lp.ph.S > 1 ? align256(4 * (size_t)lp.ph.S * m * out_f) : 0;
     lp.total = lp.off_img + align256(2 * (size_t)m * in_f);
@@ -817,34 +1334,62 @@ inline LinPlan plan_linear(int64_t m, int64_t in_f, int64_t out_f) {
 }
 
 template <int CB, int MODE>
-hipError_t set_lds_cap() {
-    // well below the 160 KB per workgroup, leaving room for static LDS
-    hipError_t e = hipFuncSetAttribute((const void*)gemv_kernel<CB, MODE>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
-    if (e != hipSuccess) (void)hipGetLastError();  // do not leave a sticky error behind
-    return e;
-}
-
-hipError_t init_lds_caps() {
-    static const hipError_t st = [] {
-        hipError_t e = hipSuccess;
-        hipError_t r[] = {set_lds_cap<0, 0>(), set_lds_cap<0, 1>(), set_lds_cap<0, 2>(),
-                          set_lds_cap<0, 3>(), set_lds_cap<1, 0>(), set_lds_cap<1, 1>(),
-                          set_lds_cap<1, 2>(), set_lds_cap<1, 3>(), set_lds_cap<2, 0>(),
-                          set_lds_cap<2, 1>(), set_lds_cap<2, 2>(), set_lds_cap<2, 3>()};
-        for (hipError_t x : r)
-            if (x != hipSuccess) e = x;
+hipError_t launch_wg(int grid, size_t lds, hipStream_t st, const GemvParams& p) {
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute((const void*)gemv_wg_kernel<CB, MODE>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (e != hipSuccess) (void)hipGetLastError();
         return e;
     }();
-    return st;
+    if (attr != hipSuccess) return attr;
+    gemv_wg_kernel<CB, MODE><<<grid, kThreads, lds, st>>>(p);
+    return hipGetLastError();
+}
+
+// One GEMV instance: its dynamic-LDS cap is raised once (well below the
+// 160 KB per workgroup; the launches stay under 54 KB), then it is launched.
+template <int CB, int MODE, int LK>
+hipError_t launch_one(int grid, size_t lds, hipStream_t st, const GemvParams& p) {
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute((const void*)gemv_kernel<CB, MODE, LK>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (e != hipSuccess) (void)hipGetLastError();  // do not leave a sticky error behind
+        return e;
+    }();
+    if (attr != hipSuccess) return attr;
+    gemv_kernel<CB, MODE, LK><<<grid, kThreads, lds, st>>>(p);
+    return hipGetLastError();
+}
+
+// lk: the launch's uniform bit width (lane-linear stage layout), or 0 for a
+// mixed-K MoE phase (per-expert K, padded stage layout).
+template <int MODE, int CB>
+hipError_t launch_lk(int lk, int grid, size_t lds, hipStream_t st, const GemvParams& p) {
+    switch (lk) {
+        case 2: return launch_one<CB, MODE, 2>(grid, lds, st, p);
+        case 3: return launch_one<CB, MODE, 3>(grid, lds, st, p);
+        case 4: return launch_one<CB, MODE, 4>(grid, lds, st, p);
+        default:
+            if constexpr (MODE == kModeGateUp || MODE == kModeDown) return launch_one<CB, MODE, 0>(grid, lds, st, p);
+            return hipErrorInvalidValue;
+    }
 }
 
 template <int MODE>
-void launch_gemv(int cb, int grid, size_t lds, hipStream_t st, const GemvParams& p) {
+hipError_t launch_gemv(int cb, int lk, const PhasePlan& ph, hipStream_t st, const GemvParams& p) {
+    const int grid = ph.grid;
+    const size_t lds = ph.lds;
+    if (ph.wg) {
+        switch (cb) {
+            case 0: return launch_wg<0, MODE>(grid, lds, st, p);
+            case 1: return launch_wg<1, MODE>(grid, lds, st, p);
+            default: return launch_wg<2, MODE>(grid, lds, st, p);
+        }
+    }
     switch (cb) {
-        case 0: gemv_kernel<0, MODE><<<grid, kThreads, lds, st>>>(p); break;
-        case 1: gemv_kernel<1, MODE><<<grid, kThreads, lds, st>>>(p); break;
-        default: gemv_kernel<2, MODE><<<grid, kThreads, lds, st>>>(p); break;
+        case 0: return launch_lk<MODE, 0>(lk, grid, lds, st, p);
+        case 1: return launch_lk<MODE, 1>(lk, grid, lds, st, p);
+        default: return launch_lk<MODE, 2>(lk, grid, lds, st, p);
     }
 }
 
@@ -874,11 +1419,11 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
                "trellis dimensions must reconstruct whole 128-element Hadamard blocks");
     EXL3_CHECK(tiles_k * 16 <= (1 << 24) && tiles_n * 16 <= (1 << 24), "feature dimensions too large");
     EXL3_CHECK(x && trellis && suh && svh && out, "null pointer argument");
+    EXL3_CHECK(tiles_k * tiles_n * 32 * K < (1ll << 31), "packed trellis must be smaller than 2 GiB");
     const int64_t in_f = tiles_k * 16, out_f = tiles_n * 16;
     const LinPlan lp = plan_linear(m, in_f, out_f);
     EXL3_CHECK(workspace_bytes >= (int64_t)lp.total && workspace,
                "workspace too small: need %zu bytes", lp.total);
-    EXL3_HIP(init_lds_caps());
     uint16_t* img = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(workspace) + lp.off_img);
     RotateArgs ra = {};
     ra.x = x;
@@ -900,13 +1445,13 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     p.in_features = (int)in_f;
     p.out_features = (int)out_f;
     p.m_rows = (int)m;
+    p.max_groups = (int)((m + lp.MRB - 1) / lp.MRB);
     p.out = out;
     p.out_dtype = out_dtype;
     p.out_stride = out_f;
     p.S = lp.ph.S;
     p.R_hb = lp.ph.R_hb;
     p.C_hb = lp.ph.C_hb;
-    p.NJ = lp.ph.NJ;
     p.MRB = lp.MRB;
     p.n_rows_ws = (int)m;
     p.ws = reinterpret_cast<float*>(workspace);
@@ -917,8 +1462,7 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
     EXL3_LAUNCHED();
     profile_mark(1, st);
-    launch_gemv<kModeLinear>(codebook, (int)(out_f / 128 / lp.ph.NJ) * lp.ph.S, lp.ph.lds, st, p);
-    EXL3_LAUNCHED();
+    EXL3_HIP(launch_gemv<kModeLinear>(codebook, (int)K, lp.ph, st, p));
     profile_mark(2, st);
     if (lp.ph.S > 1) {
         const int items = (int)(m * (out_f / 128));
@@ -939,7 +1483,8 @@ struct BatchPlan {
 inline BatchPlan plan_batched(int64_t m, int64_t n_sel, int64_t in_f, int64_t out_f) {
     BatchPlan bp;
     bp.MRB = (int)(m < kMaxMRB ? m : kMaxMRB);
-    bp.ph = plan_phase((int)in_f, (int)out_f, (int)n_sel, bp.MRB);
+    const int groups = (int)(n_sel * ((m + bp.MRB - 1) / bp.MRB));
+    bp.ph = plan_phase((int)in_f, (int)out_f, groups, groups, (int)n_sel, bp.MRB);
     // [split partials (S > 1)][rotated input rows per slot, fp16]
     bp.off_img = bp.ph.S > 1 ? align256(4 * (size_t)bp.ph.S * n_sel * m * out_f) : 0;
     bp.total = bp.off_img + align256(2 * (size_t)n_sel * m * in_f);
@@ -974,7 +1519,6 @@ EXL3_API int exl3_gemv_batched(const void* x, int x_dtype, int64_t m, int64_t in
     const BatchPlan bp = plan_batched(m, n_sel, in_features, out_features);
     EXL3_CHECK(workspace && workspace_bytes >= (int64_t)bp.total,
                "workspace too small: need %zu bytes", bp.total);
-    EXL3_HIP(init_lds_caps());
     uint16_t* img = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(workspace) + bp.off_img);
     RotateArgs ra = {};
     ra.x = x;
@@ -999,6 +1543,7 @@ EXL3_API int exl3_gemv_batched(const void* x, int x_dtype, int64_t m, int64_t in
     p.in_features = (int)in_features;
     p.out_features = (int)out_features;
     p.max_slots = (int)n_sel;
+    p.max_groups = (int)(n_sel * ((m + bp.MRB - 1) / bp.MRB));
     p.expert_list = expert_indices;
     p.n_ptr = (int)n_ptr;
     p.batch_m = (int)m;
@@ -1008,7 +1553,6 @@ EXL3_API int exl3_gemv_batched(const void* x, int x_dtype, int64_t m, int64_t in
     p.S = bp.ph.S;
     p.R_hb = bp.ph.R_hb;
     p.C_hb = bp.ph.C_hb;
-    p.NJ = bp.ph.NJ;
     p.MRB = bp.MRB;
     p.n_rows_ws = (int)(n_sel * m);
     p.ws = reinterpret_cast<float*>(workspace);
@@ -1016,9 +1560,7 @@ EXL3_API int exl3_gemv_batched(const void* x, int x_dtype, int64_t m, int64_t in
     const int64_t rot_units = n_sel * m * (in_features / 128);
     rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
     EXL3_LAUNCHED();
-    launch_gemv<kModeBatched>(codebook, (int)(n_sel * (out_features / 128 / bp.ph.NJ) * bp.ph.S),
-                              bp.ph.lds, st, p);
-    EXL3_LAUNCHED();
+    EXL3_HIP(launch_gemv<kModeBatched>(codebook, (int)K, bp.ph, st, p));
     if (bp.ph.S > 1) {
         const int64_t items = n_sel * m * (out_features / 128);
         FinishBatch fb{svh_tab, expert_indices, (int)m, (int)n_ptr};
@@ -1058,6 +1600,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     EXL3_CHECK(inter > 0 && inter % 128 == 0,
                "fused MoE local intermediate width must be a positive multiple of 128");
     EXL3_CHECK(hidden <= (1 << 20) && inter <= (1 << 20), "fused MoE dimensions too large");
+    EXL3_CHECK(hidden * inter / 2 < (1ll << 31), "fused MoE expert projections must pack below 2 GiB");
     EXL3_CHECK(std::isfinite(swiglu_limit) && swiglu_limit >= 0.0f,
                "fused MoE SwiGLU limit must be finite and nonnegative (0 disables clipping)");
     EXL3_CHECK(codebook >= 0 && codebook <= 2, "codebook must be 0 (3INST), 1 (MCG) or 2 (mul1)");
@@ -1078,7 +1621,6 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     const MoePlan mp = plan_moe(T, topk, n_local, hidden, inter, gateless);
     EXL3_CHECK(workspace && workspace_bytes >= (int64_t)mp.total,
                "fused MoE workspace too small: need %zu bytes", mp.total);
-    EXL3_HIP(init_lds_caps());
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
 
@@ -1093,12 +1635,16 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     ro.row_token = ro.slot_rows + mp.max_slots;
     ro.row_expert = ro.row_token + mp.n_routes;
     ro.route_pos = ro.row_expert + mp.n_routes;
+    ro.n_mtiles = ro.route_pos + mp.n_routes;  // row groups of MRB rows
+    ro.mt_slot = ro.n_mtiles + 1;
+    ro.mt_row0 = ro.mt_slot + mp.max_groups;
+    ro.mt_expert = ro.mt_row0 + mp.max_groups;
     if (n_local <= kRouteMaxLocal) {
-        EXL3_HIP(launch_route(ids, ids_dtype, mp.n_routes, (int)topk, (int)n_local, n_valid, 0, ro,
+        EXL3_HIP(launch_route(ids, ids_dtype, mp.n_routes, (int)topk, (int)n_local, n_valid, mp.MRB, ro,
                               st));
     } else {
         route_bitonic_kernel<<<1, kRouteThreads, 0, st>>>(ids, ids_dtype, mp.n_routes, (int)topk,
-                                                          (int)n_local, n_valid, ro);
+                                                          (int)n_local, n_valid, mp.MRB, ro);
         EXL3_LAUNCHED();
     }
 
@@ -1117,6 +1663,11 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     p.slot_start = ro.slot_start;
     p.slot_rows = ro.slot_rows;
     p.row_token = ro.row_token;
+    p.n_groups = ro.n_mtiles;
+    p.group_slot = ro.mt_slot;
+    p.group_row0 = ro.mt_row0;
+    p.group_expert = ro.mt_expert;
+    p.max_groups = mp.max_groups;
     p.max_slots = mp.max_slots;
     p.MRB = mp.MRB;
     p.n_rows_ws = mp.n_routes;
@@ -1158,12 +1709,12 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pg.S = mp.gu.S;
     pg.R_hb = mp.gu.R_hb;
     pg.C_hb = mp.gu.C_hb;
-    pg.NJ = mp.gu.NJ;
     pg.ws = ws_gu;
     profile_mark(2, st);
-    launch_gemv<kModeGateUp>(codebook, mp.max_slots * (int)(inter / 128 / mp.gu.NJ) * mp.gu.S * mp.nproj,
-                             mp.gu.lds, st, pg);
-    EXL3_LAUNCHED();
+    // uniform K over the streamed projections: the lane-linear stage layout
+    const int lk_gu = gateless ? (kt[1] ? 0 : (int)Ks[1])
+                               : ((!kt[0] && !kt[1] && Ks[0] == Ks[1]) ? (int)Ks[0] : 0);
+    EXL3_HIP(launch_gemv<kModeGateUp>(codebook, lk_gu, mp.gu, st, pg));
 
     // down input rows: gate/up finished once per route
     GemvParams pd = p;
@@ -1174,7 +1725,6 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pd.S = mp.dn.S;
     pd.R_hb = mp.dn.R_hb;
     pd.C_hb = mp.dn.C_hb;
-    pd.NJ = mp.dn.NJ;
     pd.ws = ws_d;
     pd.x = img_d;
     pd.x_dtype = kF16;
@@ -1187,9 +1737,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
 
     // down: raw partials [S_d][routes][hidden]
     profile_mark(4, st);
-    launch_gemv<kModeDown>(codebook, mp.max_slots * (int)(hidden / 128 / mp.dn.NJ) * mp.dn.S, mp.dn.lds, st,
-                           pd);
-    EXL3_LAUNCHED();
+    EXL3_HIP(launch_gemv<kModeDown>(codebook, kt[2] ? 0 : (int)Ks[2], mp.dn, st, pd));
 
     profile_mark(5, st);
     combine_kernel<<<(int)(T * (hidden / 128)), kCombineWaves * 64, 0, st>>>(

@@ -64,6 +64,13 @@ struct GemvParams {
     const int* slot_start;
     const int* slot_rows;
     const int* row_token;
+    // Row groups of the slots (MRB rows each; the router's row tiles): the
+    // persistent GEMV's units are (group, projection, split, column block).
+    const int* n_groups;
+    const int* group_slot;
+    const int* group_row0;
+    const int* group_expert;
+    int max_groups;
     int max_slots;
     int m_rows;  // linear: number of rows
     // Batched (one linear per listed expert, same input rows): the expert of
@@ -85,7 +92,6 @@ struct GemvParams {
     int S;         // splits of the input dimension
     int R_hb;      // 128-row Hadamard blocks per split
     int C_hb;      // Hadamard blocks whose activations are staged at once
-    int NJ;        // 128-column blocks per workgroup (activations staged once)
     int MRB;       // rows per row group (<= 16)
     int n_rows_ws; // rows addressed in the workspace (route rows or m)
     float* ws;
@@ -120,23 +126,64 @@ __device__ __forceinline__ int pi_inv(int r) {
 // MFMA column nu -> tile column.
 __device__ __forceinline__ int sigma_col(int n) { return (n >> 1) | ((n & 1) << 3); }
 
-struct LaneWords {
+// Per-lane geometry of a tile row at bit width K (computed when K changes).
+// Stage layout LK: for a launch whose K is uniform (LK = K) the staged tile
+// row is lane-linear, tile t at t*32K bytes (conflict-free writes, K-specific
+// immediate read offsets); for mixed-K launches (LK = 0) each tile sits at a
+// 128-byte slot of the 1 KB stage (a 32K-byte tile is a whole number of
+// 16-byte pieces, so every lane's piece lies in one tile), so one loop serves
+// every K.
+struct LaneGeo {
+    uint32_t voff;    // the lane's 16 bytes of the row (lanes past the 256K-byte span: 0)
+    uint32_t wr;      // LDS offset of that piece in the stage (lanes past the span: 0, same bytes)
     uint32_t off_hi;  // byte offset (in a tile) of the word holding the earlier bits
     uint32_t off_lo;  // byte offset of the word holding the last bit
     uint32_t shift;   // funnel shift that puts the last window at bit 0
 };
 
-template <int K>
-__device__ __forceinline__ LaneWords lane_words(int lane) {
-    constexpr int n32 = 8 * K;
+// Bytes between consecutive tiles of a staged tile row.
+template <int LK>
+__device__ __forceinline__ constexpr int stage_tile_stride() { return LK ? 32 * LK : 128; }
+
+// The padded (LK = 0) layout's geometry from the lane id with no division
+// (K uniform, 2..4): lane / 2K as a reciprocal multiply (exact for lane < 64),
+// the modulo of the word index as a select.
+__device__ __forceinline__ LaneGeo lane_geo_padded(int K, uint32_t lane) {
+    LaneGeo g;
+    const uint32_t pieces = 16u * K, per_tile = 2u * K;
+    const uint32_t magic = K == 2 ? 64u : (K == 3 ? 43u : 32u);
+    const uint32_t tl = (lane * magic) >> 8;
+    const bool in = lane < pieces;
+    g.voff = in ? lane * 16u : 0u;
+    g.wr = in ? tl * 128u + (lane - tl * per_tile) * 16u : 0u;
+    const int q = lane_q((int)lane);
+    const int E = (4 * q + 4) * K;
+    const int wb = (E - 1) >> 5;
+    g.off_lo = 4u * wb;
+    g.off_hi = 4u * (wb == 0 ? 8 * K - 1 : wb - 1);
+    g.shift = 32u * (wb + 1) - E;
+    return g;
+}
+
+template <int LK>
+__device__ __forceinline__ LaneGeo lane_geo(int K, int lane) {
+    LaneGeo g;
+    const int pieces = 16 * K;  // 16-byte pieces per tile row (8 tiles of 32K bytes)
+    g.voff = lane < pieces ? lane * 16 : 0;
+    if constexpr (LK != 0) {
+        g.wr = g.voff;
+    } else {
+        const int per_tile = 2 * K;
+        g.wr = lane < pieces ? (lane / per_tile) * 128 + (lane % per_tile) * 16 : 0;
+    }
+    const int n32 = 8 * K;
     const int q = lane_q(lane);
     const int E = (4 * q + 4) * K;  // end (exclusive) of the lane's last window
     const int wb = (E - 1) >> 5;
-    LaneWords w;
-    w.off_lo = 4u * wb;
-    w.off_hi = 4u * ((wb + n32 - 1) % n32);
-    w.shift = 32u * (wb + 1) - E;
-    return w;
+    g.off_lo = 4u * wb;
+    g.off_hi = 4u * ((wb + n32 - 1) % n32);
+    g.shift = 32u * (wb + 1) - E;
+    return g;
 }
 
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
@@ -161,20 +208,22 @@ __device__ __forceinline__ uint32_t hash32(uint32_t w) {
 }
 
 // Decode the lane's four weights of one tile into MFMA B registers (each a
-// (lo, hi) fp16 pair whose sum is the weight).  Per weight, for the two
-// "sum of halves" codebooks: one bit-field extract of the window, one
-// full-rate multiply for the hash and one v_bitop3 for the mask/xor: three
-// VALU ops per weight (plus one funnel shift per four weights).
-template <int K, int CB>
-__device__ __forceinline__ void decode4(uint32_t hi, uint32_t lo, uint32_t shift, uint32_t b[4]) {
+// (lo, hi) fp16 pair whose sum is the weight).  sh1/sh2/sh3 = 3K/2K/K are the
+// wave-uniform shifts of the earlier windows.  Per weight, for the two "sum
+// of halves" codebooks: one bit-field extract of the window, one full-rate
+// multiply for the hash and one v_bitop3 for the mask/xor: three VALU ops per
+// weight (plus one funnel shift per four weights).
+template <int CB>
+__device__ __forceinline__ void decode4(uint32_t hi, uint32_t lo, uint32_t shift, uint32_t sh3,
+                                        uint32_t sh2, uint32_t sh1, uint32_t b[4]) {
     const uint32_t s = __builtin_amdgcn_alignbit(hi, lo, shift);
+    const uint32_t w[4] = {(s >> sh3) & 0xFFFFu, (s >> sh2) & 0xFFFFu, (s >> sh1) & 0xFFFFu, s & 0xFFFFu};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t w = (s >> ((3 - i) * K)) & 0xFFFFu;
         if constexpr (CB == kCbMul1) {
-            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(w));  // (value, +0)
+            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(w[i]));  // (value, +0)
         } else {
-            b[i] = (hash32<CB>(w) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+            b[i] = (hash32<CB>(w[i]) & 0x8FFF8FFFu) ^ 0x3B603B60u;
         }
     }
 }

@@ -21,6 +21,7 @@ struct RouteOut {
     int* mt_slot;      // [max_mtiles]
     int* mt_row0;      // [max_mtiles]
     int* n_sorted;     // [1] routes kept (nullable)
+    int* mt_expert;    // [max_mtiles] local expert of each row tile (nullable)
 };
 
 // Upper bound of the row tiles produced for tile_rows-row tiles.

@@ -145,6 +145,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_multisplit_kernel(
         const int mt0 = block_exclusive_scan(nt, tmp, &n_mt);
         for (int k = 0; k < nt; ++k) {
             o.mt_slot[mt0 + k] = slot;
+            if (o.mt_expert) o.mt_expert[mt0 + k] = d;
             o.mt_row0[mt0 + k] = k * tile_rows;
         }
         if (threadIdx.x == 0) o.n_mtiles[0] = n_mt;
