@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes of one gate/up launch at T=16 (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000,
 # factors from a 256 MiB copy), from profiles/moe_decode_c1_t16.md; re-measured
 # with rocprofv3 --pmc whenever the kernel changes.
-GATE_UP_TRAFFIC_T16 = 145_198_779 + 3_966_159
+GATE_UP_TRAFFIC_T16 = 144_855_404 + 1_572_864
 
 
 def cpu_model() -> str:
@@ -371,7 +371,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_kernel<3INST, gate/up>",
+            "kernel": "gemv_wg_kernel<3INST, gate/up>",
             "achieved": round(head["gate_up_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

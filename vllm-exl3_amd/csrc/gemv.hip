@@ -5,16 +5,25 @@
 //   * exl3_gemv / exl3_gemm (csrc/exl3_gemv.cu:23-63, csrc/exl3_gemm.cu:8-31,
 //     bindings csrc/bindings.cpp:110-147);
 //   * the fused decode MoE p2b_fused_moe{,_mk,_padded}
-//     (csrc/p2b_moe.cu:643-1071, 1295-2487) as four ordinary launches, no
+//     (csrc/p2b_moe.cu:643-1071, 1295-2487) as six ordinary launches, no
 //     grid barriers, no device-scope fences, no host synchronisation:
-//       route    stable sort of the routes by expert (one workgroup);
+//       route    stable sort of the routes by expert (one workgroup), with
+//                the slots' row groups of MRB rows;
+//       rotate   each kept route's gate/up input rows, rotated once (suh,
+//                128-Hadamard, fp16) into the GEMV's image order;
 //       gate/up  raw split-K partial sums of both projections;
-//       down     its activation staging finishes gate/up (sum of splits,
-//                output rotation x svh, fp16 rounding, SwiGLU, down suh,
-//                down input rotation), then raw split-K partial sums;
+//       act      finishes gate/up per route (sum of splits, output rotation
+//                x svh, fp16 rounding, activation, down suh, down input
+//                rotation);
+//       down     raw split-K partial sums;
 //       combine  per (token, column block): finish each route's down result
 //                (rotation x svh) and sum w * d in slot order
 //                (csrc/p2b_moe.cu:1976-2008): deterministic, no atomics.
+// The GEMV phases run one of two kernels chosen by the planner: one unit per
+// workgroup (gemv_wg_kernel) when the units fill at most a couple of rounds
+// of resident workgroups, else the persistent gemv_kernel, which streams a
+// balanced range of units per workgroup with its trellis pipeline kept full
+// across them.
 #include "gemv_core.h"
 #include "profile.h"
 #include "route.h"

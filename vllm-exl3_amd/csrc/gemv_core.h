@@ -1,12 +1,17 @@
 // Streaming EXL3 decode-GEMV core for gfx950 (small row counts: decode).
 //
-// One workgroup (4 wave64s) owns one 128-column block of one or two
-// projections over a K-split range of input rows, for every activation row of
-// one routing slot (or of the plain linear).  Per wave, per tile row (8 packed
-// 16x16 tiles = 256*K contiguous bytes):
-//   * one coalesced 128-bit global load per lane into registers, software
-//     pipelined kDepth rows ahead, then one ds_write_b128 into the wave's LDS
-//     slot (no workgroup barrier in the main loop);
+// A unit of work is one 128-column block of one projection over a K-split
+// range of input rows for one row group (up to MRB activation rows of one
+// routing slot, or of the plain linear).  Two kernels stream units (gemv.hip):
+// one unit per workgroup for launches that fill at most a couple of rounds
+// of resident workgroups, and a persistent kernel that streams a contiguous
+// range of units per workgroup with the trellis pipeline kept full across
+// them.  Per wave, per tile row (8 packed 16x16 tiles = 256*K contiguous
+// bytes):
+//   * one coalesced 128-bit load per lane (a scalar buffer resource for the
+//     wave's rows, the row advance as the scalar offset) into registers,
+//     software pipelined kDepth rows ahead, then one ds_write_b128 into the
+//     wave's LDS slot (no workgroup barrier in the main loop);
 //   * each lane reads the two uint32 words that cover the windows of its four
 //     consecutive tile indices, funnel-shifts them once, and decodes four
 //     weights with bfe / one full-rate 32-bit multiply / bitop3 each;
