@@ -6,26 +6,25 @@
 // src/vllm_exl3/exl3.py:2981-3599, which sort on the host and loop over fat
 // experts in Python).
 //
-// GEMM tile: one 256-thread workgroup (4 wave64s in a 2x2 grid) owns 256 rows
-// x 256 output columns of one expert; each wave accumulates 128x128 with
-// v_mfma_f32_16x16x32_f16.  Per 32-deep k-step, the packed trellis of the
-// step (2 tile rows x 16 tiles) is decoded ONCE by the workgroup into an LDS
-// B tile of real fp16 weights (the codebook's two halves summed with one
-// packed fp16 add, which rounds the exact sum once like the reference's
-// decoder) and reused by every row of the tile.  Thread t decodes the 32
-// weights of one 8-index group of one tile: for such a group the window
-// offsets inside the group's K+1 words are compile-time constants, so the
-// decode needs no dynamic register indexing.  The four 16-byte units it
-// produces are eight consecutive k of one column: exactly one MFMA B-operand
-// lane fragment, stored with one ds_write_b128.
+// GEMM tile: one 512-thread workgroup (8 wave64s in a 2x4 grid, two per
+// SIMD) owns 256 rows x 256 output columns of one expert; each wave
+// accumulates 128x64 with v_mfma_f32_16x16x32_f16.  Per 32-deep k-step, the
+// packed trellis of the step (2 tile rows x 16 tiles) is decoded ONCE by the
+// workgroup into an LDS B tile of real fp16 weights (the codebook's two
+// halves summed with one packed fp16 add, which rounds the exact sum once
+// like the reference's decoder) and reused by every row of the tile.  Two
+// threads share the 32 weights of one 8-index group of one tile, one column
+// half each: for such a group the window offsets inside the group's K+1
+// words are compile-time constants, so the decode needs no dynamic register
+// indexing; each 16-byte unit produced is eight consecutive k of one column,
+// exactly one MFMA B-operand lane fragment, stored with one ds_write_b128.
 //
-// Pipeline (one barrier per k-step, two LDS stages): global loads of A rows
-// and packed bits run kLoadSets k-steps ahead of their staging, the operand
-// fragments of step s+1 are read from LDS while the MFMAs of step s run, and
-// the decode of step s+2 is issued in the same basic block as those MFMAs so
-// the scheduler can overlap VALU decode with matrix-core work.  Waves whose
-// 128-row slice holds no rows of the expert skip their MFMAs but still share
-// the decode.
+// Pipeline (one barrier per k-step, three LDS stages): global loads of A rows
+// and packed bits run two k-steps ahead of their staging; iteration t reads
+// the operands of step t, decodes and stages step t + 2 and issues the MFMAs
+// of step t, and the other wave on the SIMD fills the MFMA and LDS latencies.
+// Waves whose 128-row slice holds no rows of the expert skip their MFMAs but
+// still share the decode.
 //
 // The output rotation is not done in the GEMM epilogue: the GEMM stores
 // Z / sqrt(128) (Z = A x Wq) and the consumer kernel - the activation kernel,
@@ -42,15 +41,11 @@
 namespace exl3 {
 namespace {
 
-constexpr int kFatThreads = 256;  // 4 waves; each stages, decodes and multiplies
 constexpr int kTM = 256;          // rows per tile
 constexpr int kTN = 256;          // output columns per tile
 constexpr int kTK = 32;           // k per step (two tile rows)
 constexpr int kABytes = kTM * kTK * 2;  // A stage: [256 rows][32 k] fp16, 64 B per row
 constexpr int kBBytes = kTN * kTK * 2;  // B stage: [256 cols][32 k] fp16, 64 B per column
-constexpr int kStages = 2;
-constexpr int kLoadSets = 2;      // k-steps of global loads in flight, in registers
-constexpr int kFatLds = kStages * (kABytes + kBBytes);  // 64 KB
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const v4u* gv4p;
@@ -81,7 +76,17 @@ struct FatParams {
     const int* slot_start;
     const int* slot_rows;
     int n_ntiles;
-    int n_tiles;                  // max_mtiles * n_ntiles (grid before XCD rounding)
+    int n_tiles;                  // nproj * max_mtiles * n_ntiles (grid before XCD rounding)
+    // Grouped launches may cover two projections of the same shape (the MoE
+    // gate and up): tiles [n_tiles / 2, n_tiles) use these operands.  One
+    // launch for both fills the workgroup rounds that two launches would
+    // each leave part-empty.
+    int nproj;
+    const uint16_t* a2;
+    const int64_t* trellis_tab2;
+    const int8_t* ktab2;
+    int kuni2;
+    void* out2;
 };
 
 // Decoded (lo, hi) half pair of one window for the sum-of-halves codebooks,
@@ -143,28 +148,6 @@ struct PairGeom {
 // g in 0..7 for the decoded B units).
 __device__ __forceinline__ int swz(int r, int c) { return r * 64 + (((c ^ (r >> 2) ^ (r >> 3)) & 3) << 4); }
 
-// Decode all 32 weights of group g of a tile from the group's K + 1 stream
-// words w[] (word F + j, F = g K - 1, wrapping) and store the four 8-k units
-// (one 16-byte MFMA operand fragment each): unit (b1, b2) is column
-// col0 + 8 b2, chunk c0 + b1 of the B stage.
-template <int K, int CB>
-__device__ __forceinline__ void decode_group(const uint32_t (&w)[K + 1], uint8_t* B, int col0, int c0) {
-#pragma unroll
-    for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-        for (int b1 = 0; b1 < 2; ++b1) {
-            v4u u;
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const int rel = PairGeom<K>::rel(b1, b2, p);
-                const uint32_t s =
-                    __builtin_amdgcn_alignbit(w[rel - 1], w[rel], PairGeom<K>::shift(b1, b2, p));
-                u[p] = decode_pair<K, CB>(s);
-            }
-            *reinterpret_cast<v4u*>(B + swz(col0 + 8 * b2, c0 + b1)) = u;
-        }
-}
-
 // LDS-only barrier: the stage buffers are handed over through LDS, and the
 // global prefetches must stay in flight across it.
 __device__ __forceinline__ void lds_barrier() {
@@ -179,209 +162,37 @@ struct FatTile {
     const uint8_t* trellis;
 };
 
-// One 256 x 256 output tile.  Wave w = (wm, wn) multiplies row fragments
-// wm, wm + 2, ..., (MF of them, 16 rows each) by column fragments
-// 8 wn .. 8 wn + 7.  k-step t lives in LDS stage t & 1 and in global-load
-// register set t % kLoadSets.  Iteration s, in one basic block:
-//   * reads the operand fragments of step s + 1 (LDS stage (s + 1) & 1),
-//   * stages step s + 2 into LDS stage s & 1 from its register set: four
-//     16-byte A chunks and the decode of one trellis group (32 weights,
-//     four B units),
-//   * issues the global loads of step s + 2 + kLoadSets into that set,
-//   * issues the MFMAs of step s on the operands read in iteration s - 1,
-// and the scheduler spreads the decode VALU work between the MFMAs.  The
-// LDS-only barrier at the end of the iteration also waits for this wave's
-// reads of step s + 1, so stage s & 1 is free for step s + 3 ... and the
-// operands are in registers when the next iteration's MFMAs issue.
-template <int CB, int K, int MF>
-__device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, uint8_t* lds) {
-    constexpr int tile_bytes = 32 * K;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int wm = w >> 1, wn = w & 1;
-    const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
-    const int tiles_n = p.N >> 4;
-
-    // ---- staging roles.  Global loads go through buffer resources whose
-    // base is wave-uniform; the per-step advance is the scalar offset.
-    const int ac = tid & 3, ar0 = tid >> 2;  // A: chunk ac of rows ar0 + 64 j
-    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.a + ft.a_row0 * p.lda), (short)0, 0x7FFFFFFF, 0x00020000);
-    int a_voff[4];
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-        a_voff[jj] = (int)((min(ar0 + 64 * jj, ft.rows_valid - 1) * p.lda + 8 * ac) * 2);
-    const int t_idx = tid >> 3, g = tid & 7;  // decode: group g of tile (tr, tc)
-    const int tr = t_idx >> 4, tc = t_idx & 15;
-    // a last tile of 128 columns: the upper half decodes a copy of the last
-    // valid tile column (in bounds; those B columns are never multiplied)
-    const int tcols = min(16, tiles_n - ft.nt * 16);
-    const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(ft.trellis + (size_t)ft.nt * 16 * tile_bytes), (short)0, 0x7FFFFFFF, 0x00020000);
-    const int t_voff = (tr * tiles_n + min(tc, tcols - 1)) * tile_bytes;
-    const int step_bytes = 2 * tiles_n * tile_bytes;
-    int w_voff[K + 1];
-#pragma unroll
-    for (int j = 0; j < K + 1; ++j) {
-        const int idx = g * K - 1 + j;
-        w_voff[j] = t_voff + 4 * (idx < 0 ? idx + 8 * K : idx);
-    }
-    const int col0 = tc * 16 + g;
-
-    v4u ga[kLoadSets][4];
-    uint32_t gw[kLoadSets][K + 1];
-    auto load = [&](int t, int r) {
-        const int so = min(t, nsteps - 1);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-            ga[r][jj] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff[jj], so * (kTK * 2), 0));
-#pragma unroll
-        for (int j = 0; j < K + 1; ++j)
-            gw[r][j] = __builtin_amdgcn_raw_buffer_load_b32(trs, w_voff[j], so * step_bytes, 0);
-    };
-    auto stage = [&](int st, int r) {
-        uint8_t* A = lds + st * kABytes;
-        uint8_t* B = lds + kStages * kABytes + st * kBBytes;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[r][jj];
-        decode_group<K, CB>(gw[r], B, col0, 2 * tr);
-    };
-
-    constexpr int MFA = MF > 0 ? MF : 1;
-    float4_t acc[MFA][8];
-#pragma unroll
-    for (int i = 0; i < MFA; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-    half8_t fa[2][MFA], fb[2][8];
-    // operand fragment offsets (the swizzle key of a 16-row fragment depends
-    // on the parity of the fragment index)
-    const int off_ev = swz(lane & 15, lane >> 4), off_od = swz(16 + (lane & 15), lane >> 4) - 16 * 64;
-    auto read = [&](int st, int o) {
-        const uint8_t* A = lds + st * kABytes;
-        const uint8_t* B = lds + kStages * kABytes + st * kBBytes;
-#pragma unroll
-        for (int nf = 0; nf < 8; ++nf) {
-            const int f = 8 * wn + nf;
-            fb[o][nf] = *reinterpret_cast<const half8_t*>(B + f * 1024 + ((f & 1) ? off_od : off_ev));
-        }
-#pragma unroll
-        for (int i = 0; i < MF; ++i) {
-            const int f = wm + 2 * i;
-            fa[o][i] = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
-        }
-    };
-    auto mma = [&](int o) {
-#pragma unroll
-        for (int i = 0; i < MF; ++i)
-#pragma unroll
-            for (int nf = 0; nf < 8; ++nf)
-                acc[i][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[o][i], fb[o][nf], acc[i][nf], 0, 0, 0);
-        // issue order: the operand reads first, then every MFMA followed by
-        // a few VALU ops of the decode, so the matrix core and the VALU work
-        // side by side
-        __builtin_amdgcn_sched_group_barrier(0x100, 8 + MF, 0);  // DS read
-#pragma unroll
-        for (int i = 0; i < 8 * MF; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-        }
-    };
-
-    // ---- prologue: stages 0 and 1 hold steps 0 and 1, register sets hold
-    // steps 2 .. kLoadSets + 1, operand set 0 holds step 0.  The second
-    // barrier lets every wave finish reading stage 0 before step 2
-    // overwrites it.
-    load(0, 0);
-    load(1, 1);
-    stage(0, 0);
-    stage(1, 1);
-#pragma unroll
-    for (int t = 2; t < kLoadSets + 2; ++t) load(t, t % kLoadSets);
-    lds_barrier();
-    if constexpr (MF > 0) read(0, 0);
-    lds_barrier();
-
-    // ---- main loop, kLoadSets k-steps per trip (nsteps is a multiple of 4)
-    for (int s = 0; s < nsteps; s += kLoadSets) {
-#pragma unroll
-        for (int u = 0; u < kLoadSets; ++u) {
-            const int r = (u + 2) % kLoadSets;  // register set of step s + u + 2
-            if constexpr (MF > 0) read((u + 1) & 1, (u + 1) & 1);
-            stage(u & 1, r);
-            load(s + u + 2 + kLoadSets, r);
-            if constexpr (MF > 0) mma(u & 1);
-            lds_barrier();
-        }
-    }
-
-    // ---- epilogue: Z * out_scale for the valid rows
-    if constexpr (MF > 0) {
-        const int colw = ft.nt * kTN + 128 * wn + (lane & 15);
-#pragma unroll
-        for (int i = 0; i < MF; ++i) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 16 * (wm + 2 * i) + 4 * (lane >> 4) + e;
-                if (r < ft.rows_valid) {
-                    const int64_t o = (ft.out_row0 + r) * p.ldo + colw;
-#pragma unroll
-                    for (int nf = 0; nf < 8; ++nf) {
-                        const float v = acc[i][nf][e] * p.out_scale;
-                        if (p.out_f32)
-                            reinterpret_cast<float*>(p.out)[o + nf * 16] = v;
-                        else
-                            reinterpret_cast<uint16_t*>(p.out)[o + nf * 16] = half_to_bits((half_t)v);
-                    }
-                }
-            }
-        }
-    }
-}
-
-template <int CB, int K>
-__device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft, uint8_t* lds) {
-    // row fragments of this wave holding valid rows (wave row half wm takes
-    // fragments wm, wm + 2, ...), rounded up to 0, 1, 2, 4 or 8
-    const int wm = (threadIdx.x >> 6) >> 1, wn = (threadIdx.x >> 6) & 1;
-    const int nfr = (ft.rows_valid + 15) >> 4;
-    const bool cols_ok = wn * 128 < p.N - ft.nt * kTN;  // a last tile may hold 128 columns
-    const int mine = (nfr > wm && cols_ok) ? (nfr - wm + 1) >> 1 : 0;
-    if (mine == 0)
-        fat_tile<CB, K, 0>(p, ft, lds);
-    else if (mine == 1)
-        fat_tile<CB, K, 1>(p, ft, lds);
-    else if (mine == 2)
-        fat_tile<CB, K, 2>(p, ft, lds);
-    else if (mine <= 4)
-        fat_tile<CB, K, 4>(p, ft, lds);
-    else
-        fat_tile<CB, K, 8>(p, ft, lds);
-}
-
-template <int CB>
-__global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void fat_gemm_kernel(
-    FatParams p) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    // XCD-aware order: consecutive logical tiles (the N tiles of one row tile,
-    // which share their A rows) land on the same XCD and its L2.
+// The tile of this workgroup (false: none).  XCD-aware order: consecutive
+// logical tiles (the N tiles of one row tile, which share their A rows) land
+// on the same XCD and its L2.  pq: the projection's operands.
+__device__ __forceinline__ bool fat_tile_of(const FatParams& p, FatParams& pq, FatTile& ft, int& K) {
     const int G = p.n_tiles;
     const int per = (G + 7) >> 3;
-    const int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (logical >= G) return;
+    int logical = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (logical >= G) return false;
+    if (p.nproj > 1) {
+        const int per_q = G / p.nproj;
+        if (logical >= per_q) {
+            logical -= per_q;
+            pq.a = p.a2;
+            pq.trellis_tab = p.trellis_tab2;
+            pq.ktab = p.ktab2;
+            pq.kuni = p.kuni2;
+            pq.out = p.out2;
+        }
+    }
     const int mt = logical / p.n_ntiles;
-    FatTile ft;
     ft.nt = logical % p.n_ntiles;
-    int K;
     if (p.grouped) {
-        if (mt >= *p.n_mtiles) return;
+        if (mt >= *p.n_mtiles) return false;
         const int slot = p.mt_slot[mt];
         const int row0 = p.mt_row0[mt];
         const int e = p.slot_expert[slot];
         ft.a_row0 = (int64_t)p.slot_start[slot] + row0;
         ft.out_row0 = ft.a_row0;
         ft.rows_valid = min(kTM, p.slot_rows[slot] - row0);
-        ft.trellis = reinterpret_cast<const uint8_t*>(p.trellis_tab[e]);
-        K = p.ktab ? (int)p.ktab[e] : p.kuni;
+        ft.trellis = reinterpret_cast<const uint8_t*>(pq.trellis_tab[e]);
+        K = pq.ktab ? (int)pq.ktab[e] : pq.kuni;
     } else {
         ft.a_row0 = (int64_t)mt * kTM;
         ft.out_row0 = ft.a_row0;
@@ -389,12 +200,7 @@ __global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(1, 
         ft.trellis = p.trellis;
         K = p.kuni;
     }
-    switch (K) {
-        case 2: fat_tile_k<CB, 2>(p, ft, lds); break;
-        case 3: fat_tile_k<CB, 3>(p, ft, lds); break;
-        case 4: fat_tile_k<CB, 4>(p, ft, lds); break;
-        default: break;  // rejected on the host
-    }
+    return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -425,9 +231,40 @@ __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
     return (uint32_t)half_to_bits(f32_to_f16_rne(a)) | ((uint32_t)half_to_bits(f32_to_f16_rne(b)) << 16);
 }
 
+// Elements i, i+1 (i even) of an fp16 array as one 4-byte load.
+__device__ __forceinline__ void ld_pair_f16(const uint16_t* p, int64_t i, float& a, float& b) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(p + i);
+    a = (float)bits_to_half((uint16_t)(v & 0xFFFFu));
+    b = (float)bits_to_half((uint16_t)(v >> 16));
+}
+
+// load_act of elements i, i+1 (i even) with one load: fp16 as is, bf16 and
+// fp32 rounded to fp16 (the reference casts activations to fp16).
+__device__ __forceinline__ void ld_act_pair(const void* x, int dtype, int64_t i, float& a, float& b) {
+    if (dtype == kF16) {
+        ld_pair_f16(reinterpret_cast<const uint16_t*>(x), i, a, b);
+    } else if (dtype == kBF16) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + i);
+        a = (float)f32_to_f16_rne(__builtin_bit_cast(float, v << 16));
+        b = (float)f32_to_f16_rne(__builtin_bit_cast(float, v & 0xFFFF0000u));
+    } else {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        const f2 v = *reinterpret_cast<const f2*>(reinterpret_cast<const float*>(x) + i);
+        a = (float)f32_to_f16_rne(v.x);
+        b = (float)f32_to_f16_rne(v.y);
+    }
+}
+
+// The row kernels below give each wave kRowBlocks consecutive 128-blocks of
+// one row and issue every load of those blocks before the first butterfly
+// (block indices past the row clamp to its last block, in bounds; only the
+// stores are predicated): one wave per (row, block) left each wave a single
+// short dependent load chain, and the launch latency-bound.
+constexpr int kRowBlocks = 8;
+
 // Gate/up input rotation of every sorted route row: A_q[row] =
 // fp16(had128(fp16(x[token]) * suh_q[expert]) / sqrt(128)) for q in gate, up.
-// One wave per (row, 128-column block).
+// One wave per (row, kRowBlocks 128-column blocks).
 __global__ __launch_bounds__(256) void rotate_in_kernel(const void* x, int x_dtype, int64_t x_stride,
                                                         int H, const int* n_sorted,
                                                         const int* row_token, const int* row_expert,
@@ -437,20 +274,30 @@ __global__ __launch_bounds__(256) void rotate_in_kernel(const void* x, int x_dty
     const int lane = threadIdx.x & 63;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (unit >= n_units) return;
-    const int nb = H >> 7;
-    const int row = (int)(unit / nb), j = (int)(unit % nb);
+    const int nb = H >> 7, ng = (nb + kRowBlocks - 1) / kRowBlocks;
+    const int row = (int)(unit / ng), j0 = (int)(unit % ng) * kRowBlocks;
     if (row >= *n_sorted) return;
+    const int jn = min(kRowBlocks, nb - j0);
     const int64_t tok = row_token[row];
     const int e = row_expert[row];
-    const int c = j * 128 + 2 * lane;
-    const float x0 = load_act(x, x_dtype, tok * x_stride + c);
-    const float x1 = load_act(x, x_dtype, tok * x_stride + c + 1);
+    float xa[kRowBlocks], xb[kRowBlocks];
+#pragma unroll
+    for (int i = 0; i < kRowBlocks; ++i)
+        ld_act_pair(x, x_dtype, tok * x_stride + (j0 + min(i, jn - 1)) * 128 + 2 * lane, xa[i], xb[i]);
     for (int q = 0; q < nproj; ++q) {
         const uint16_t* su = reinterpret_cast<const uint16_t*>(q ? suh_u[e] : suh_g[e]);
-        float a = x0 * h2f(su, c), b = x1 * h2f(su, c + 1);
-        had128_pair(a, b, lane);
-        uint16_t* dst = q ? a_u : a_g;
-        *reinterpret_cast<uint32_t*>(dst + (int64_t)row * H + c) = pack_f16(a * kHadNorm, b * kHadNorm);
+        uint16_t* dst = (q ? a_u : a_g) + (int64_t)row * H;
+        float sa[kRowBlocks], sb[kRowBlocks];
+#pragma unroll
+        for (int i = 0; i < kRowBlocks; ++i) ld_pair_f16(su, (j0 + min(i, jn - 1)) * 128 + 2 * lane, sa[i], sb[i]);
+#pragma unroll
+        for (int i = 0; i < kRowBlocks; ++i) {
+            if (i >= jn) break;  // wave-uniform
+            float a = xa[i] * sa[i], b = xb[i] * sb[i];
+            had128_pair(a, b, lane);
+            const int c = (j0 + i) * 128 + 2 * lane;
+            *reinterpret_cast<uint32_t*>(dst + c) = pack_f16(a * kHadNorm, b * kHadNorm);
+        }
     }
 }
 
@@ -474,6 +321,7 @@ __device__ __forceinline__ float activate(float g, float u, int act, float limit
 // of the intermediate dimension, g = fp16(had(Yg) * svh_g), u likewise,
 // a = fp16(act(g, u)), A_d = fp16(had(a * suh_d) / sqrt(128)).  Y holds
 // Z / sqrt(128) from the GEMM.  A_d is written over Y_g (same positions).
+// One wave per (row, kRowBlocks blocks).
 __global__ __launch_bounds__(256) void act_kernel(const int* n_sorted, const int* row_expert, int I,
                                                   const int64_t* svh_g, const int64_t* svh_u,
                                                   const int64_t* suh_d, int gateless, int act,
@@ -482,36 +330,56 @@ __global__ __launch_bounds__(256) void act_kernel(const int* n_sorted, const int
     const int lane = threadIdx.x & 63;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (unit >= n_units) return;
-    const int nb = I >> 7;
-    const int row = (int)(unit / nb), j = (int)(unit % nb);
+    const int nb = I >> 7, ng = (nb + kRowBlocks - 1) / kRowBlocks;
+    const int row = (int)(unit / ng), j0 = (int)(unit % ng) * kRowBlocks;
     if (row >= *n_sorted) return;
+    const int jn = min(kRowBlocks, nb - j0);
     const int e = row_expert[row];
-    const int c = j * 128 + 2 * lane;
-    const int64_t o = (int64_t)row * I + c;
-    float u0 = h2f(y_u, o), u1 = h2f(y_u, o + 1);
-    had128_pair(u0, u1, lane);
     const uint16_t* svu = reinterpret_cast<const uint16_t*>(svh_u[e]);
-    u0 = (float)f32_to_f16_rne(u0 * h2f(svu, c));
-    u1 = (float)f32_to_f16_rne(u1 * h2f(svu, c + 1));
-    float g0 = 0.f, g1 = 0.f;
-    if (!gateless) {
-        g0 = h2f(y_g, o);
-        g1 = h2f(y_g, o + 1);
-        had128_pair(g0, g1, lane);
-        const uint16_t* svg = reinterpret_cast<const uint16_t*>(svh_g[e]);
-        g0 = (float)f32_to_f16_rne(g0 * h2f(svg, c));
-        g1 = (float)f32_to_f16_rne(g1 * h2f(svg, c + 1));
-    }
+    const uint16_t* svg = reinterpret_cast<const uint16_t*>(svh_g[e]);
     const uint16_t* sud = reinterpret_cast<const uint16_t*>(suh_d[e]);
-    float a0 = (float)f32_to_f16_rne(activate(g0, u0, act, limit)) * h2f(sud, c);
-    float a1 = (float)f32_to_f16_rne(activate(g1, u1, act, limit)) * h2f(sud, c + 1);
-    had128_pair(a0, a1, lane);
-    *reinterpret_cast<uint32_t*>(y_g + o) = pack_f16(a0 * kHadNorm, a1 * kHadNorm);
+    float u0[kRowBlocks], u1[kRowBlocks], g0[kRowBlocks], g1[kRowBlocks];
+    float vu0[kRowBlocks], vu1[kRowBlocks], vg0[kRowBlocks], vg1[kRowBlocks], d0[kRowBlocks], d1[kRowBlocks];
+#pragma unroll
+    for (int i = 0; i < kRowBlocks; ++i) {
+        const int c = (j0 + min(i, jn - 1)) * 128 + 2 * lane;
+        const int64_t o = (int64_t)row * I + c;
+        ld_pair_f16(y_u, o, u0[i], u1[i]);
+        ld_pair_f16(svu, c, vu0[i], vu1[i]);
+        ld_pair_f16(sud, c, d0[i], d1[i]);
+        if (!gateless) {
+            ld_pair_f16(y_g, o, g0[i], g1[i]);
+            ld_pair_f16(svg, c, vg0[i], vg1[i]);
+        } else {
+            g0[i] = g1[i] = vg0[i] = vg1[i] = 0.f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kRowBlocks; ++i) {
+        if (i >= jn) break;  // wave-uniform
+        float a0 = u0[i], a1 = u1[i];
+        had128_pair(a0, a1, lane);
+        const float uu0 = (float)f32_to_f16_rne(a0 * vu0[i]);
+        const float uu1 = (float)f32_to_f16_rne(a1 * vu1[i]);
+        float gg0 = 0.f, gg1 = 0.f;
+        if (!gateless) {
+            float b0 = g0[i], b1 = g1[i];
+            had128_pair(b0, b1, lane);
+            gg0 = (float)f32_to_f16_rne(b0 * vg0[i]);
+            gg1 = (float)f32_to_f16_rne(b1 * vg1[i]);
+        }
+        float r0 = (float)f32_to_f16_rne(activate(gg0, uu0, act, limit)) * d0[i];
+        float r1 = (float)f32_to_f16_rne(activate(gg1, uu1, act, limit)) * d1[i];
+        had128_pair(r0, r1, lane);
+        const int64_t o = (int64_t)row * I + (j0 + i) * 128 + 2 * lane;
+        *reinterpret_cast<uint32_t*>(y_g + o) = pack_f16(r0 * kHadNorm, r1 * kHadNorm);
+    }
 }
 
 // out[t, block] = sum over the token's routes, in slot order, of
 // w * had(Y_d[pos]) * svh_d (Y_d = Z / sqrt(128)); sentinel routes skipped.
-// One wave per (token, 128-column block): deterministic, no atomics.
+// One wave per (token, kRowBlocks 128-column blocks): deterministic, no
+// atomics; per route, the loads of all the wave's blocks are issued first.
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_d, int H, int T,
                                                               int topk, const int* route_pos,
                                                               const int* row_expert,
@@ -519,16 +387,16 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_
                                                               int w_dtype, void* out, int out_dtype) {
     const int lane = threadIdx.x & 63;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int nb = H >> 7;
-    if (unit >= (int64_t)T * nb) return;
-    const int t = (int)(unit / nb), j = (int)(unit % nb);
-    const int c = j * 128 + 2 * lane;
-    float s0 = 0.f, s1 = 0.f;
+    const int nb = H >> 7, ng = (nb + kRowBlocks - 1) / kRowBlocks;
+    if (unit >= (int64_t)T * ng) return;
+    const int t = (int)(unit / ng), j0 = (int)(unit % ng) * kRowBlocks;
+    const int jn = min(kRowBlocks, nb - j0);
+    float s0[kRowBlocks], s1[kRowBlocks];
+#pragma unroll
+    for (int i = 0; i < kRowBlocks; ++i) s0[i] = s1[i] = 0.f;
     for (int k = 0; k < topk; ++k) {
         const int pos = route_pos[(int64_t)t * topk + k];
         if (pos < 0) continue;  // wave-uniform
-        float v0 = h2f(y_d, (int64_t)pos * H + c), v1 = h2f(y_d, (int64_t)pos * H + c + 1);
-        had128_pair(v0, v1, lane);
         const uint16_t* sv = reinterpret_cast<const uint16_t*>(svh_d[row_expert[pos]]);
         const int64_t wi = (int64_t)t * topk + k;
         float w;
@@ -538,11 +406,27 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_
             w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wi]);
         else
             w = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wi] << 16);
-        s0 += w * (v0 * h2f(sv, c));
-        s1 += w * (v1 * h2f(sv, c + 1));
+        float v0[kRowBlocks], v1[kRowBlocks], h0[kRowBlocks], h1[kRowBlocks];
+#pragma unroll
+        for (int i = 0; i < kRowBlocks; ++i) {
+            const int c = (j0 + min(i, jn - 1)) * 128 + 2 * lane;
+            ld_pair_f16(y_d, (int64_t)pos * H + c, v0[i], v1[i]);
+            ld_pair_f16(sv, c, h0[i], h1[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kRowBlocks; ++i) {
+            had128_pair(v0[i], v1[i], lane);
+            s0[i] += w * (v0[i] * h0[i]);
+            s1[i] += w * (v1[i] * h1[i]);
+        }
     }
-    store_out(out, out_dtype, (int64_t)t * H + c, s0);
-    store_out(out, out_dtype, (int64_t)t * H + c + 1, s1);
+#pragma unroll
+    for (int i = 0; i < kRowBlocks; ++i) {
+        if (i >= jn) break;  // wave-uniform
+        const int c = (j0 + i) * 128 + 2 * lane;
+        store_out(out, out_dtype, (int64_t)t * H + c, s0[i]);
+        store_out(out, out_dtype, (int64_t)t * H + c + 1, s1[i]);
+    }
 }
 
 // Drop-in output pass: rows of Z / sqrt(128) (fp32, in `src`) ->
@@ -572,6 +456,210 @@ __global__ __launch_bounds__(256) void fat_out_kernel(const float* src, int M, i
         if (d < 0 || d >= out_rows) return;  // wave-uniform: rows outside out are dropped
         atomicAdd(out + d * N + c, w * v0);
         atomicAdd(out + d * N + c + 1, w * v1);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The GEMM tile: 256 x 256 outputs computed by 8 waves (2 row halves x 4
+// column quarters, 128 x 64 each, 128 accumulator registers), two waves per
+// SIMD, so that the decode VALU of one runs beside the other's MFMAs (a
+// wave's own MFMAs and VALU do not overlap; with one 128 x 128 wave per SIMD
+// they ran back to back).  Operands are read from LDS just before their MFMAs
+// (single-buffered: the other wave covers the latency), so three LDS stages
+// keep one barrier per k-step: step t lives in stage t % 3; iteration t reads
+// step t, stages step t + 2 (into the stage step t - 1 used, whose reads all
+// waves finished before the previous barrier), issues the global loads of
+// step t + 4 and runs the MFMAs of step t.  Staging: two 16-byte A chunks
+// per thread; each trellis group is decoded by two threads, one per column
+// half (waves 0-3 take half 0, waves 4-7 half 1, so the choice is uniform
+// per wave).
+constexpr int kFatThreads = 512;
+constexpr int kStages = 3;
+constexpr int kFatLds = kStages * (kABytes + kBBytes);  // 96 KB
+
+template <int K, int CB, int B2>
+__device__ __forceinline__ void decode_group_half(const uint32_t (&w)[K + 1], uint8_t* B, int col0, int c0) {
+#pragma unroll
+    for (int b1 = 0; b1 < 2; ++b1) {
+        v4u u;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int rel = PairGeom<K>::rel(b1, B2, p);
+            const uint32_t s = __builtin_amdgcn_alignbit(w[rel - 1], w[rel], PairGeom<K>::shift(b1, B2, p));
+            u[p] = decode_pair<K, CB>(s);
+        }
+        *reinterpret_cast<v4u*>(B + swz(col0 + 8 * B2, c0 + b1)) = u;
+    }
+}
+
+template <int CB, int K, int MF>
+__device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, uint8_t* lds) {
+    constexpr int tile_bytes = 32 * K;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w & 1, wn = w >> 1;
+    const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
+    const int tiles_n = p.N >> 4;
+
+    // ---- staging roles
+    const int ac = tid & 3, ar0 = tid >> 2;  // A: chunk ac of rows ar0 and ar0 + 128
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.a + ft.a_row0 * p.lda), (short)0, 0x7FFFFFFF, 0x00020000);
+    int a_voff[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+        a_voff[jj] = (int)((min(ar0 + 128 * jj, ft.rows_valid - 1) * p.lda + 8 * ac) * 2);
+    const int gt = tid & 255;                     // decode: group of this thread
+    const bool hi_half = w >= 4;                  // column half of the group (wave-uniform)
+    const int t_idx = gt >> 3, g = gt & 7;
+    const int tr = t_idx >> 4, tc = t_idx & 15;
+    const int tcols = min(16, tiles_n - ft.nt * 16);
+    const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(ft.trellis + (size_t)ft.nt * 16 * tile_bytes), (short)0, 0x7FFFFFFF, 0x00020000);
+    const int t_voff = (tr * tiles_n + min(tc, tcols - 1)) * tile_bytes;
+    const int step_bytes = 2 * tiles_n * tile_bytes;
+    int w_voff[K + 1];
+#pragma unroll
+    for (int j = 0; j < K + 1; ++j) {
+        const int idx = g * K - 1 + j;
+        w_voff[j] = t_voff + 4 * (idx < 0 ? idx + 8 * K : idx);
+    }
+    const int col0 = tc * 16 + g;
+
+    v4u ga[2][2];
+    uint32_t gw[2][K + 1];
+    auto load = [&](int t, int r) {
+        const int so = min(t, nsteps - 1);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+            ga[r][jj] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff[jj], so * (kTK * 2), 0));
+#pragma unroll
+        for (int j = 0; j < K + 1; ++j)
+            gw[r][j] = __builtin_amdgcn_raw_buffer_load_b32(trs, w_voff[j], so * step_bytes, 0);
+    };
+    auto stage = [&](int st, int r) {
+        uint8_t* A = lds + st * kABytes;
+        uint8_t* B = lds + kStages * kABytes + st * kBBytes;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 128 * jj, ac)) = ga[r][jj];
+        if (hi_half)
+            decode_group_half<K, CB, 1>(gw[r], B, col0, 2 * tr);
+        else
+            decode_group_half<K, CB, 0>(gw[r], B, col0, 2 * tr);
+    };
+
+    constexpr int MFA = MF > 0 ? MF : 1;
+    float4_t acc[MFA][4];
+#pragma unroll
+    for (int i = 0; i < MFA; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    half8_t fa[MFA], fb[4];
+    const int off_ev = swz(lane & 15, lane >> 4), off_od = swz(16 + (lane & 15), lane >> 4) - 16 * 64;
+    auto read = [&](int st) {
+        const uint8_t* A = lds + st * kABytes;
+        const uint8_t* B = lds + kStages * kABytes + st * kBBytes;
+#pragma unroll
+        for (int nf = 0; nf < 4; ++nf) {
+            const int f = 4 * wn + nf;
+            fb[nf] = *reinterpret_cast<const half8_t*>(B + f * 1024 + ((f & 1) ? off_od : off_ev));
+        }
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+            const int f = wm + 2 * i;
+            fa[i] = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
+        }
+    };
+    auto mma = [&]() {
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int nf = 0; nf < 4; ++nf)
+                acc[i][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[nf], acc[i][nf], 0, 0, 0);
+    };
+
+    // ---- prologue: stages 0, 1 hold steps 0, 1; register sets hold steps 2, 3
+    load(0, 0);
+    load(1, 1);
+    stage(0, 0);
+    stage(1, 1);
+    load(2, 0);
+    load(3, 1);
+    lds_barrier();
+
+    // ---- main loop, two k-steps per trip (nsteps is a multiple of 4)
+    int st_cur = 0;  // stage of step t
+    for (int t = 0; t < nsteps; t += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int st_next2 = st_cur == 0 ? 2 : st_cur - 1;  // (t + u + 2) % 3
+            if constexpr (MF > 0) read(st_cur);
+            stage(st_next2, u);
+            load(t + u + 4, u);
+            if constexpr (MF > 0) mma();
+            lds_barrier();
+            st_cur = st_cur == 2 ? 0 : st_cur + 1;
+        }
+    }
+
+    // ---- epilogue: Z * out_scale for the valid rows
+    if constexpr (MF > 0) {
+        const int colw = ft.nt * kTN + 64 * wn + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 16 * (wm + 2 * i) + 4 * (lane >> 4) + e;
+                if (r < ft.rows_valid) {
+                    const int64_t o = (ft.out_row0 + r) * p.ldo + colw;
+#pragma unroll
+                    for (int nf = 0; nf < 4; ++nf) {
+                        const float v = acc[i][nf][e] * p.out_scale;
+                        if (p.out_f32)
+                            reinterpret_cast<float*>(p.out)[o + nf * 16] = v;
+                        else
+                            reinterpret_cast<uint16_t*>(p.out)[o + nf * 16] = half_to_bits((half_t)v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int CB, int K>
+__device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft, uint8_t* lds) {
+    // row fragments of this wave holding valid rows (row half wm takes
+    // fragments wm, wm + 2, ...), rounded up to 0, 1, 2, 4 or 8
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int wm = w & 1, wn = w >> 1;
+    const int nfr = (ft.rows_valid + 15) >> 4;
+    const bool cols_ok = wn * 64 < p.N - ft.nt * kTN;  // a last tile may hold 128 columns
+    const int mine = (nfr > wm && cols_ok) ? (nfr - wm + 1) >> 1 : 0;
+    if (mine == 0)
+        fat_tile<CB, K, 0>(p, ft, lds);
+    else if (mine == 1)
+        fat_tile<CB, K, 1>(p, ft, lds);
+    else if (mine == 2)
+        fat_tile<CB, K, 2>(p, ft, lds);
+    else if (mine <= 4)
+        fat_tile<CB, K, 4>(p, ft, lds);
+    else
+        fat_tile<CB, K, 8>(p, ft, lds);
+}
+
+template <int CB>
+__global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fat_gemm_kernel(
+    FatParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    FatTile ft;
+    int K;
+    FatParams pq = p;
+    if (!fat_tile_of(p, pq, ft, K)) return;
+    switch (K) {
+        case 2: fat_tile_k<CB, 2>(pq, ft, lds); break;
+        case 3: fat_tile_k<CB, 3>(pq, ft, lds); break;
+        case 4: fat_tile_k<CB, 4>(pq, ft, lds); break;
+        default: break;  // rejected on the host
     }
 }
 
@@ -796,7 +884,7 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
 
     profile_mark(1, st);
     {
-        const int64_t units = (int64_t)pp.n_routes * (hidden / 128);
+        const int64_t units = (int64_t)pp.n_routes * ((hidden / 128 + kRowBlocks - 1) / kRowBlocks);
         rotate_in_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
             x, x_dtype, hidden, (int)hidden, n_sorted, ro.row_token, ro.row_expert,
             gateless ? up_suh : gate_suh, up_suh, nproj, gateless ? a_u : a_g, a_u, units);
@@ -818,21 +906,25 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
     p.slot_start = ro.slot_start;
     p.slot_rows = ro.slot_rows;
     p.n_ntiles = (int)((inter + kTN - 1) / kTN);
-    p.n_tiles = pp.max_mtiles * p.n_ntiles;
-    for (int q = 0; q < nproj; ++q) {
-        const bool up = gateless || q == 1;
-        p.a = up ? a_u : a_g;
-        p.trellis_tab = up ? up_trellis : gtab_t;
-        p.ktab = up ? k_up : k_gate;
-        p.kuni = (int)(up ? K_up : K_gate);
-        p.out = up ? y_u : y_g;
-        launch_fat(codebook, p, st);
-        EXL3_LAUNCHED();
-    }
+    // gate and up in one launch (tiles of the second half use the up operands)
+    p.nproj = nproj;
+    p.n_tiles = nproj * pp.max_mtiles * p.n_ntiles;
+    p.a = gateless ? a_u : a_g;
+    p.trellis_tab = gateless ? up_trellis : gtab_t;
+    p.ktab = gateless ? k_up : k_gate;
+    p.kuni = (int)(gateless ? K_up : K_gate);
+    p.out = gateless ? y_u : y_g;
+    p.a2 = a_u;
+    p.trellis_tab2 = up_trellis;
+    p.ktab2 = k_up;
+    p.kuni2 = (int)K_up;
+    p.out2 = y_u;
+    launch_fat(codebook, p, st);
+    EXL3_LAUNCHED();
     (void)gtab_su;
     profile_mark(3, st);
     {
-        const int64_t units = (int64_t)pp.n_routes * (inter / 128);
+        const int64_t units = (int64_t)pp.n_routes * ((inter / 128 + kRowBlocks - 1) / kRowBlocks);
         act_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
             n_sorted, ro.row_expert, (int)inter, gtab_sv, up_svh, down_suh, gateless, act,
             swiglu_limit, gateless ? y_u : y_g, y_u, units);
@@ -850,12 +942,13 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
     p.out = y_d;
     p.ldo = hidden;
     p.n_ntiles = (int)((hidden + kTN - 1) / kTN);
+    p.nproj = 1;
     p.n_tiles = pp.max_mtiles * p.n_ntiles;
     launch_fat(codebook, p, st);
     EXL3_LAUNCHED();
     profile_mark(5, st);
     {
-        const int64_t units = T * (hidden / 128);
+        const int64_t units = T * ((hidden / 128 + kRowBlocks - 1) / kRowBlocks);
         prefill_combine_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
             y_d, (int)hidden, (int)T, (int)topk, ro.route_pos, ro.row_expert, down_svh, weights,
             w_dtype, out, out_dtype);
