@@ -25,3 +25,12 @@ def gpu():
 
     _lib.load()  # raises when the library is not built
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(params=["auto", "persistent"])
+def gemv_policy(request, monkeypatch):
+    """Decode GEMV kernel choice for the test: the cost model's ("auto"), or
+    the persistent kernel forced (EXL3_GEMV_KERNEL, read by the library's
+    planner on every call), so both kernels are checked on the same inputs."""
+    monkeypatch.setenv("EXL3_GEMV_KERNEL", request.param)
+    return request.param

@@ -26,7 +26,7 @@ def _run(lin, x, cb, gpu, out_dtype=torch.float16):
 @pytest.mark.parametrize("K", [2, 3, 4])
 @pytest.mark.parametrize("cb", [0, 1, 2])
 @pytest.mark.parametrize("m", [1, 3, 16, 21])
-def test_gemm_small_vs_oracle(gpu, K, cb, m):
+def test_gemm_small_vs_oracle(gpu, gemv_policy, K, cb, m):
     lin = S.linear(3000 + 100 * K + 10 * cb + m, 384, 256, K)
     x = S.activations(7 + m, m, 384)
     w = O.dequant(lin["trellis"], lin["suh"], lin["svh"], K, cb)
@@ -36,7 +36,7 @@ def test_gemm_small_vs_oracle(gpu, K, cb, m):
 
 
 @pytest.mark.parametrize("m", [1, 16])
-def test_gemm_config0_full_size(gpu, m):
+def test_gemm_config0_full_size(gpu, gemv_policy, m):
     # in=out=2048, K4, MCG, bf16 activations, m in {1, 16}
     lin = S.linear(0, 2048, 2048, 4)
     x = S.activations(1, m, 2048)
@@ -81,7 +81,7 @@ def _batched_layer(gpu, seed, n, in_f, out_f, K):
 
 
 @pytest.mark.parametrize("K,cb,m", [(2, 1, 1), (3, 0, 5), (4, 2, 3)])
-def test_gemv_batched_vs_oracle_and_sequential(gpu, K, cb, m):
+def test_gemv_batched_vs_oracle_and_sequential(gpu, gemv_policy, K, cb, m):
     # p2b_gemv_batched: entry i == exl3_gemv(x, W[idx_i]); repeated ids, and an
     # id outside the tables gives zeros (csrc/p2b_batched.cu:341-368)
     packs, dev, tabs = _batched_layer(gpu, 4000 + 10 * K + cb, 4, 512, 256, K)
@@ -100,7 +100,7 @@ def test_gemv_batched_vs_oracle_and_sequential(gpu, K, cb, m):
         assert (got[i].float() - seq.float()).abs().max().item() <= 1e-3
 
 
-def test_gemv_batched_reference_shape_and_split_path(gpu):
+def test_gemv_batched_reference_shape_and_split_path(gpu, gemv_policy):
     # the reference's test shape: 8 experts, K2 MCG, 4096 -> 2048, m = 1
     # (long input dimension: the split-K finisher path)
     packs, dev, tabs = _batched_layer(gpu, 5000, 8, 4096, 2048, 2)

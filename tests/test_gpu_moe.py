@@ -29,7 +29,7 @@ def _forward(dev_layer, x, ids, w, E, I, cb, K=(3, 3, 3), mixed=False, **kw):
 
 @pytest.mark.parametrize("cb", [0, 1, 2])
 @pytest.mark.parametrize("T", [1, 3, 16])
-def test_moe_small_vs_oracle(gpu, cb, T):
+def test_moe_small_vs_oracle(gpu, gemv_policy, cb, T):
     E, H, I, topk = 6, 256, 384, 4
     experts = _layer(40 + T + cb, E, H, I, 3, cb)
     x = S.activations(5 + T, T, H)
@@ -42,7 +42,7 @@ def test_moe_small_vs_oracle(gpu, cb, T):
 
 
 @pytest.mark.parametrize("limit", [0.0, 1.0, 10.0])
-def test_moe_clamp_repeated_ids_zero_weight(gpu, limit):
+def test_moe_clamp_repeated_ids_zero_weight(gpu, gemv_policy, limit):
     # Mirrors the reference's contract fixture (tests/test_native_moe_contract.py:
     # 54-151): two experts, repeated routes, last route zero weight, output
     # scales chosen so clipping engages.
@@ -70,7 +70,7 @@ def test_moe_clamp_repeated_ids_zero_weight(gpu, limit):
     assert rel_l2(got, want) <= TOL
 
 
-def test_moe_mixed_k_and_sentinels(gpu):
+def test_moe_mixed_k_and_sentinels(gpu, gemv_policy):
     E, H, I, topk, T = 8, 384, 256, 4, 5
     ks = [(2, 3, 4), 3, 4, (4, 2, 3), 2, 3, 4, 2]
     experts = _layer(91, E, H, I, ks, 1)
@@ -85,7 +85,22 @@ def test_moe_mixed_k_and_sentinels(gpu):
     assert rel_l2(got, want) <= TOL
 
 
-def test_moe_gateless_relu2(gpu):
+def test_moe_mixed_k_whole_blocks(gpu, gemv_policy):
+    # widths that are multiples of 512: every chunk takes the GEMV's
+    # branch-free path, including the switch to an expert of another K
+    E, H, I, topk, T = 8, 1024, 512, 4, 12
+    ks = [2, 3, 4, (4, 2, 3), 2, 4, 3, (2, 4, 3)]
+    experts = _layer(93, E, H, I, ks, 0)
+    x = S.activations(10, T, H)
+    ids, w = S.softmax_topk(14, T, E, topk)
+    want = O.moe_reference(x, ids, w, dense_cpu(experts, 0))
+    dl = S.to_device(experts, gpu)
+    got = _forward(dl, torch.from_numpy(x).to(gpu).bfloat16(), torch.from_numpy(ids).to(gpu),
+                   torch.from_numpy(w).to(gpu), E, I, 0, mixed=True)
+    assert rel_l2(got, want) <= TOL
+
+
+def test_moe_gateless_relu2(gpu, gemv_policy):
     E, H, I, topk, T = 4, 256, 256, 2, 3
     experts = _layer(31, E, H, I, 3, 1, gateless=True)
     x = S.activations(4, T, H)
@@ -97,7 +112,7 @@ def test_moe_gateless_relu2(gpu):
     assert rel_l2(got, want) <= TOL
 
 
-def test_moe_swiglu_oai(gpu):
+def test_moe_swiglu_oai(gpu, gemv_policy):
     E, H, I, topk, T = 4, 256, 256, 2, 2
     experts = _layer(32, E, H, I, 4, 1)
     x = S.activations(6, T, H)
@@ -210,7 +225,7 @@ def test_p2b_rejects_unsafe_calls_before_launch(gpu, bad):
 
 
 @pytest.mark.parametrize("T", [1, 4, 16])
-def test_moe_config1_full_size(gpu, T):
+def test_moe_config1_full_size(gpu, gemv_policy, T):
     # E64 top-8, H2048, I1536, K3, 3INST, bf16 activations
     E, H, I, topk = 64, 2048, 1536, 8
     experts = S.moe_layer(1, E, H, I, 3)

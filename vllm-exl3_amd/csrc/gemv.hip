@@ -29,6 +29,8 @@
 #include "route.h"
 
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 
 namespace exl3 {
 namespace {
@@ -1252,7 +1254,21 @@ inline PhasePlan plan_phase_wg(int in_f, int out_f, int wg_items, int MRB) {
 // costs about a memory round trip); below kMinUnitsPerWg the
 // one-unit-per-workgroup plan (wg_items = slots x streamed projections) is
 // used.
+// Kernel choice override for testing and tuning: EXL3_GEMV_KERNEL=wg or
+// =persistent forces that kernel for every GEMV phase; unset or any other
+// value selects by the cost model.  Read on every plan (host side, once per
+// call), so a process can compare both kernels on the same inputs.
+inline int gemv_kernel_policy() {
+    const char* v = std::getenv("EXL3_GEMV_KERNEL");
+    if (!v) return 0;
+    if (std::strcmp(v, "wg") == 0) return 1;
+    if (std::strcmp(v, "persistent") == 0) return 2;
+    return 0;
+}
+
 inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, int wg_items, int MRB) {
+    const int policy = gemv_kernel_policy();
+    if (policy == 1) return plan_phase_wg(in_f, out_f, wg_items, MRB);
     const int n_hb = in_f / 128, n_j = out_f / 128;
     const int cap = resident_workgroups();
     PhasePlan best = {1, n_hb, pick_chunk(n_hb, MRB), 1, 0, 0};
@@ -1277,7 +1293,7 @@ inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, i
             best = {S, R_hb, C_hb, grid, 0, 0};
         }
     }
-    if (best_per_wg < kMinUnitsPerWg) return plan_phase_wg(in_f, out_f, wg_items, MRB);
+    if (policy != 2 && best_per_wg < kMinUnitsPerWg) return plan_phase_wg(in_f, out_f, wg_items, MRB);
     best.lds = gemv_lds_bytes(best.C_hb, MRB);
     return best;
 }
