@@ -231,40 +231,128 @@ __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
     return (uint32_t)half_to_bits(f32_to_f16_rne(a)) | ((uint32_t)half_to_bits(f32_to_f16_rne(b)) << 16);
 }
 
-// Elements i, i+1 (i even) of an fp16 array as one 4-byte load.
-__device__ __forceinline__ void ld_pair_f16(const uint16_t* p, int64_t i, float& a, float& b) {
-    const uint32_t v = *reinterpret_cast<const uint32_t*>(p + i);
-    a = (float)bits_to_half((uint16_t)(v & 0xFFFFu));
-    b = (float)bits_to_half((uint16_t)(v >> 16));
-}
+// The row kernels below work on 128-blocks held as 16 lanes x 8 consecutive
+// elements: every global access is one 16-byte load or store per lane (fp32
+// data: two), the butterfly runs over the 8 in-register elements and then
+// over 4 lane bits, and a wave covers 4 blocks at a time.  Each wave takes
+// kRowGroups such four-block groups of one row (8 consecutive blocks) and
+// issues every load of them before the first butterfly; block indices past
+// the row clamp to its last block (loads stay in bounds, those lanes' stores
+// are dropped).
+constexpr int kRowGroups = 2;
+constexpr int kRowSpan = 4 * kRowGroups;  // 128-blocks per wave
 
-// load_act of elements i, i+1 (i even) with one load: fp16 as is, bf16 and
-// fp32 rounded to fp16 (the reference casts activations to fp16).
-__device__ __forceinline__ void ld_act_pair(const void* x, int dtype, int64_t i, float& a, float& b) {
-    if (dtype == kF16) {
-        ld_pair_f16(reinterpret_cast<const uint16_t*>(x), i, a, b);
-    } else if (dtype == kBF16) {
-        const uint32_t v = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + i);
-        a = (float)f32_to_f16_rne(__builtin_bit_cast(float, v << 16));
-        b = (float)f32_to_f16_rne(__builtin_bit_cast(float, v & 0xFFFF0000u));
-    } else {
-        typedef float f2 __attribute__((ext_vector_type(2)));
-        const f2 v = *reinterpret_cast<const f2*>(reinterpret_cast<const float*>(x) + i);
-        a = (float)f32_to_f16_rne(v.x);
-        b = (float)f32_to_f16_rne(v.y);
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 128-point butterfly (unnormalised, natural order) over the block held by
+// the lane's 16-lane group: element 8 * (lane % 16) + i is v[i].
+__device__ __forceinline__ void had128_x8(float v[8], int lane) {
+#pragma unroll
+    for (int b = 1; b < 8; b <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (i & b) continue;
+            const float a = v[i], c = v[i | b];
+            v[i] = a + c;
+            v[i | b] = a - c;
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float p = __shfl_xor(v[i], m, 64);
+            v[i] = (lane & m) ? p - v[i] : v[i] + p;
+        }
     }
 }
 
-// The row kernels below give each wave kRowBlocks consecutive 128-blocks of
-// one row and issue every load of those blocks before the first butterfly
-// (block indices past the row clamp to its last block, in bounds; only the
-// stores are predicated): one wave per (row, block) left each wave a single
-// short dependent load chain, and the launch latency-bound.
-constexpr int kRowBlocks = 8;
+// Elements i..i+7 (i % 8 == 0) of an fp16 array.
+__device__ __forceinline__ void ld_f16x8(const uint16_t* p, int64_t i, float v[8]) {
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(p + i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[2 * k] = (float)bits_to_half(w[k] & 0xFFFFu);
+        v[2 * k + 1] = (float)bits_to_half(w[k] >> 16);
+    }
+}
+
+// Elements i..i+7 of an activation array as fp16 values: fp16 as is, bf16
+// and fp32 rounded to fp16 (the reference casts activations to fp16).
+__device__ __forceinline__ void ld_act8(const void* x, int dtype, int64_t i, float v[8]) {
+    if (dtype == kF32) {
+        const float4_t* p = reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(x) + i);
+        const float4_t a = p[0], b = p[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[k] = (float)f32_to_f16_rne(a[k]);
+            v[4 + k] = (float)f32_to_f16_rne(b[k]);
+        }
+    } else if (dtype == kBF16) {
+        const u32x4_t w = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(x) + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = (float)f32_to_f16_rne(__builtin_bit_cast(float, w[k] << 16));
+            v[2 * k + 1] = (float)f32_to_f16_rne(__builtin_bit_cast(float, w[k] & 0xFFFF0000u));
+        }
+    } else {
+        ld_f16x8(reinterpret_cast<const uint16_t*>(x), i, v);
+    }
+}
+
+// fp16(v[k] * scale) for k = 0..7 stored at p + i with one 16-byte store.
+__device__ __forceinline__ void st_f16x8(uint16_t* p, int64_t i, const float v[8], float scale) {
+    u32x4_t w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = pack_f16(v[2 * k] * scale, v[2 * k + 1] * scale);
+    *reinterpret_cast<u32x4_t*>(p + i) = w;
+}
+
+// v[0..7] stored at element i of an fp32 / fp16 / bf16 (RNE) array.
+__device__ __forceinline__ void st_out8(void* out, int dtype, int64_t i, const float v[8]) {
+    if (dtype == kF32) {
+        float4_t* p = reinterpret_cast<float4_t*>(reinterpret_cast<float*>(out) + i);
+        p[0] = float4_t{v[0], v[1], v[2], v[3]};
+        p[1] = float4_t{v[4], v[5], v[6], v[7]};
+    } else if (dtype == kF16) {
+        st_f16x8(reinterpret_cast<uint16_t*>(out), i, v, 1.0f);
+    } else {
+        u32x4_t w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t h[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                uint32_t b = __builtin_bit_cast(uint32_t, v[2 * k + j]);
+                b += 0x7FFFu + ((b >> 16) & 1u);  // RNE to bf16 (finite values)
+                h[j] = b >> 16;
+            }
+            w[k] = h[0] | (h[1] << 16);
+        }
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + i) = w;
+    }
+}
+
+// The lane's columns in the wave's kRowSpan blocks starting at block j0 of
+// a row of nb blocks: col[g] (clamped into the row) and whether it is real.
+struct RowCols {
+    int col[kRowGroups];
+    bool ok[kRowGroups];
+};
+__device__ __forceinline__ RowCols row_cols(int j0, int nb, int lane) {
+    RowCols rc;
+#pragma unroll
+    for (int g = 0; g < kRowGroups; ++g) {
+        const int j = j0 + (lane >> 4) + 4 * g;
+        rc.ok[g] = j < nb;
+        rc.col[g] = min(j, nb - 1) * 128 + (lane & 15) * 8;
+    }
+    return rc;
+}
 
 // Gate/up input rotation of every sorted route row: A_q[row] =
 // fp16(had128(fp16(x[token]) * suh_q[expert]) / sqrt(128)) for q in gate, up.
-// One wave per (row, kRowBlocks 128-column blocks).
+// One wave per (row, kRowSpan 128-column blocks).
 __global__ __launch_bounds__(256) void rotate_in_kernel(const void* x, int x_dtype, int64_t x_stride,
                                                         int H, const int* n_sorted,
                                                         const int* row_token, const int* row_expert,
@@ -274,29 +362,34 @@ __global__ __launch_bounds__(256) void rotate_in_kernel(const void* x, int x_dty
     const int lane = threadIdx.x & 63;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (unit >= n_units) return;
-    const int nb = H >> 7, ng = (nb + kRowBlocks - 1) / kRowBlocks;
-    const int row = (int)(unit / ng), j0 = (int)(unit % ng) * kRowBlocks;
+    const int nb = H >> 7, ng = (nb + kRowSpan - 1) / kRowSpan;
+    const int row = (int)(unit / ng), j0 = (int)(unit % ng) * kRowSpan;
     if (row >= *n_sorted) return;
-    const int jn = min(kRowBlocks, nb - j0);
+    const RowCols rc = row_cols(j0, nb, lane);
     const int64_t tok = row_token[row];
     const int e = row_expert[row];
-    float xa[kRowBlocks], xb[kRowBlocks];
+    const uint16_t* su[2] = {reinterpret_cast<const uint16_t*>(suh_g[e]),
+                             reinterpret_cast<const uint16_t*>(suh_u[e])};
+    float xv[kRowGroups][8], sv[2][kRowGroups][8];
 #pragma unroll
-    for (int i = 0; i < kRowBlocks; ++i)
-        ld_act_pair(x, x_dtype, tok * x_stride + (j0 + min(i, jn - 1)) * 128 + 2 * lane, xa[i], xb[i]);
-    for (int q = 0; q < nproj; ++q) {
-        const uint16_t* su = reinterpret_cast<const uint16_t*>(q ? suh_u[e] : suh_g[e]);
+    for (int g = 0; g < kRowGroups; ++g) ld_act8(x, x_dtype, tok * x_stride + rc.col[g], xv[g]);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        if (q >= nproj) break;  // wave-uniform
+#pragma unroll
+        for (int g = 0; g < kRowGroups; ++g) ld_f16x8(su[q], rc.col[g], sv[q][g]);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        if (q >= nproj) break;
         uint16_t* dst = (q ? a_u : a_g) + (int64_t)row * H;
-        float sa[kRowBlocks], sb[kRowBlocks];
 #pragma unroll
-        for (int i = 0; i < kRowBlocks; ++i) ld_pair_f16(su, (j0 + min(i, jn - 1)) * 128 + 2 * lane, sa[i], sb[i]);
+        for (int g = 0; g < kRowGroups; ++g) {
+            float v[8];
 #pragma unroll
-        for (int i = 0; i < kRowBlocks; ++i) {
-            if (i >= jn) break;  // wave-uniform
-            float a = xa[i] * sa[i], b = xb[i] * sb[i];
-            had128_pair(a, b, lane);
-            const int c = (j0 + i) * 128 + 2 * lane;
-            *reinterpret_cast<uint32_t*>(dst + c) = pack_f16(a * kHadNorm, b * kHadNorm);
+            for (int i = 0; i < 8; ++i) v[i] = xv[g][i] * sv[q][g][i];
+            had128_x8(v, lane);
+            if (rc.ok[g]) st_f16x8(dst, rc.col[g], v, kHadNorm);
         }
     }
 }
@@ -318,10 +411,11 @@ __device__ __forceinline__ float activate(float g, float u, int act, float limit
 }
 
 // Finish gate/up and build the down input: for each sorted row and 128-block
+// Finish gate/up and build the down input: for each sorted row and 128-block
 // of the intermediate dimension, g = fp16(had(Yg) * svh_g), u likewise,
 // a = fp16(act(g, u)), A_d = fp16(had(a * suh_d) / sqrt(128)).  Y holds
 // Z / sqrt(128) from the GEMM.  A_d is written over Y_g (same positions).
-// One wave per (row, kRowBlocks blocks).
+// One wave per (row, kRowSpan blocks).
 __global__ __launch_bounds__(256) void act_kernel(const int* n_sorted, const int* row_expert, int I,
                                                   const int64_t* svh_g, const int64_t* svh_u,
                                                   const int64_t* suh_d, int gateless, int act,
@@ -330,55 +424,45 @@ __global__ __launch_bounds__(256) void act_kernel(const int* n_sorted, const int
     const int lane = threadIdx.x & 63;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (unit >= n_units) return;
-    const int nb = I >> 7, ng = (nb + kRowBlocks - 1) / kRowBlocks;
-    const int row = (int)(unit / ng), j0 = (int)(unit % ng) * kRowBlocks;
+    const int nb = I >> 7, ng = (nb + kRowSpan - 1) / kRowSpan;
+    const int row = (int)(unit / ng), j0 = (int)(unit % ng) * kRowSpan;
     if (row >= *n_sorted) return;
-    const int jn = min(kRowBlocks, nb - j0);
+    const RowCols rc = row_cols(j0, nb, lane);
     const int e = row_expert[row];
     const uint16_t* svu = reinterpret_cast<const uint16_t*>(svh_u[e]);
     const uint16_t* svg = reinterpret_cast<const uint16_t*>(svh_g[e]);
     const uint16_t* sud = reinterpret_cast<const uint16_t*>(suh_d[e]);
-    float u0[kRowBlocks], u1[kRowBlocks], g0[kRowBlocks], g1[kRowBlocks];
-    float vu0[kRowBlocks], vu1[kRowBlocks], vg0[kRowBlocks], vg1[kRowBlocks], d0[kRowBlocks], d1[kRowBlocks];
+    const int64_t ro = (int64_t)row * I;
+    float u[kRowGroups][8], g[kRowGroups][8], vu[kRowGroups][8], vg[kRowGroups][8], d[kRowGroups][8];
 #pragma unroll
-    for (int i = 0; i < kRowBlocks; ++i) {
-        const int c = (j0 + min(i, jn - 1)) * 128 + 2 * lane;
-        const int64_t o = (int64_t)row * I + c;
-        ld_pair_f16(y_u, o, u0[i], u1[i]);
-        ld_pair_f16(svu, c, vu0[i], vu1[i]);
-        ld_pair_f16(sud, c, d0[i], d1[i]);
+    for (int q = 0; q < kRowGroups; ++q) {
+        ld_f16x8(y_u, ro + rc.col[q], u[q]);
+        ld_f16x8(svu, rc.col[q], vu[q]);
+        ld_f16x8(sud, rc.col[q], d[q]);
         if (!gateless) {
-            ld_pair_f16(y_g, o, g0[i], g1[i]);
-            ld_pair_f16(svg, c, vg0[i], vg1[i]);
-        } else {
-            g0[i] = g1[i] = vg0[i] = vg1[i] = 0.f;
+            ld_f16x8(y_g, ro + rc.col[q], g[q]);
+            ld_f16x8(svg, rc.col[q], vg[q]);
         }
     }
 #pragma unroll
-    for (int i = 0; i < kRowBlocks; ++i) {
-        if (i >= jn) break;  // wave-uniform
-        float a0 = u0[i], a1 = u1[i];
-        had128_pair(a0, a1, lane);
-        const float uu0 = (float)f32_to_f16_rne(a0 * vu0[i]);
-        const float uu1 = (float)f32_to_f16_rne(a1 * vu1[i]);
-        float gg0 = 0.f, gg1 = 0.f;
-        if (!gateless) {
-            float b0 = g0[i], b1 = g1[i];
-            had128_pair(b0, b1, lane);
-            gg0 = (float)f32_to_f16_rne(b0 * vg0[i]);
-            gg1 = (float)f32_to_f16_rne(b1 * vg1[i]);
+    for (int q = 0; q < kRowGroups; ++q) {
+        had128_x8(u[q], lane);
+        if (!gateless) had128_x8(g[q], lane);
+        float r[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float uu = (float)f32_to_f16_rne(u[q][i] * vu[q][i]);
+            const float gg = gateless ? 0.f : (float)f32_to_f16_rne(g[q][i] * vg[q][i]);
+            r[i] = (float)f32_to_f16_rne(activate(gg, uu, act, limit)) * d[q][i];
         }
-        float r0 = (float)f32_to_f16_rne(activate(gg0, uu0, act, limit)) * d0[i];
-        float r1 = (float)f32_to_f16_rne(activate(gg1, uu1, act, limit)) * d1[i];
-        had128_pair(r0, r1, lane);
-        const int64_t o = (int64_t)row * I + (j0 + i) * 128 + 2 * lane;
-        *reinterpret_cast<uint32_t*>(y_g + o) = pack_f16(r0 * kHadNorm, r1 * kHadNorm);
+        had128_x8(r, lane);
+        if (rc.ok[q]) st_f16x8(y_g, ro + rc.col[q], r, kHadNorm);
     }
 }
 
 // out[t, block] = sum over the token's routes, in slot order, of
 // w * had(Y_d[pos]) * svh_d (Y_d = Z / sqrt(128)); sentinel routes skipped.
-// One wave per (token, kRowBlocks 128-column blocks): deterministic, no
+// One wave per (token, kRowSpan 128-column blocks): deterministic, no
 // atomics; per route, the loads of all the wave's blocks are issued first.
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_d, int H, int T,
                                                               int topk, const int* route_pos,
@@ -387,13 +471,15 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_
                                                               int w_dtype, void* out, int out_dtype) {
     const int lane = threadIdx.x & 63;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int nb = H >> 7, ng = (nb + kRowBlocks - 1) / kRowBlocks;
+    const int nb = H >> 7, ng = (nb + kRowSpan - 1) / kRowSpan;
     if (unit >= (int64_t)T * ng) return;
-    const int t = (int)(unit / ng), j0 = (int)(unit % ng) * kRowBlocks;
-    const int jn = min(kRowBlocks, nb - j0);
-    float s0[kRowBlocks], s1[kRowBlocks];
+    const int t = (int)(unit / ng), j0 = (int)(unit % ng) * kRowSpan;
+    const RowCols rc = row_cols(j0, nb, lane);
+    float s[kRowGroups][8];
 #pragma unroll
-    for (int i = 0; i < kRowBlocks; ++i) s0[i] = s1[i] = 0.f;
+    for (int q = 0; q < kRowGroups; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[q][i] = 0.f;
     for (int k = 0; k < topk; ++k) {
         const int pos = route_pos[(int64_t)t * topk + k];
         if (pos < 0) continue;  // wave-uniform
@@ -406,27 +492,22 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_
             w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wi]);
         else
             w = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wi] << 16);
-        float v0[kRowBlocks], v1[kRowBlocks], h0[kRowBlocks], h1[kRowBlocks];
+        float v[kRowGroups][8], h[kRowGroups][8];
 #pragma unroll
-        for (int i = 0; i < kRowBlocks; ++i) {
-            const int c = (j0 + min(i, jn - 1)) * 128 + 2 * lane;
-            ld_pair_f16(y_d, (int64_t)pos * H + c, v0[i], v1[i]);
-            ld_pair_f16(sv, c, h0[i], h1[i]);
+        for (int q = 0; q < kRowGroups; ++q) {
+            ld_f16x8(y_d, (int64_t)pos * H + rc.col[q], v[q]);
+            ld_f16x8(sv, rc.col[q], h[q]);
         }
 #pragma unroll
-        for (int i = 0; i < kRowBlocks; ++i) {
-            had128_pair(v0[i], v1[i], lane);
-            s0[i] += w * (v0[i] * h0[i]);
-            s1[i] += w * (v1[i] * h1[i]);
+        for (int q = 0; q < kRowGroups; ++q) {
+            had128_x8(v[q], lane);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s[q][i] += w * (v[q][i] * h[q][i]);
         }
     }
 #pragma unroll
-    for (int i = 0; i < kRowBlocks; ++i) {
-        if (i >= jn) break;  // wave-uniform
-        const int c = (j0 + i) * 128 + 2 * lane;
-        store_out(out, out_dtype, (int64_t)t * H + c, s0[i]);
-        store_out(out, out_dtype, (int64_t)t * H + c + 1, s1[i]);
-    }
+    for (int q = 0; q < kRowGroups; ++q)
+        if (rc.ok[q]) st_out8(out, out_dtype, (int64_t)t * H + rc.col[q], s[q]);
 }
 
 // Drop-in output pass: rows of Z / sqrt(128) (fp32, in `src`) ->
@@ -884,7 +965,7 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
 
     profile_mark(1, st);
     {
-        const int64_t units = (int64_t)pp.n_routes * ((hidden / 128 + kRowBlocks - 1) / kRowBlocks);
+        const int64_t units = (int64_t)pp.n_routes * ((hidden / 128 + kRowSpan - 1) / kRowSpan);
         rotate_in_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
             x, x_dtype, hidden, (int)hidden, n_sorted, ro.row_token, ro.row_expert,
             gateless ? up_suh : gate_suh, up_suh, nproj, gateless ? a_u : a_g, a_u, units);
@@ -924,7 +1005,7 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
     (void)gtab_su;
     profile_mark(3, st);
     {
-        const int64_t units = (int64_t)pp.n_routes * ((inter / 128 + kRowBlocks - 1) / kRowBlocks);
+        const int64_t units = (int64_t)pp.n_routes * ((inter / 128 + kRowSpan - 1) / kRowSpan);
         act_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
             n_sorted, ro.row_expert, (int)inter, gtab_sv, up_svh, down_suh, gateless, act,
             swiglu_limit, gateless ? y_u : y_g, y_u, units);
@@ -948,7 +1029,7 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
     EXL3_LAUNCHED();
     profile_mark(5, st);
     {
-        const int64_t units = T * ((hidden / 128 + kRowBlocks - 1) / kRowBlocks);
+        const int64_t units = T * ((hidden / 128 + kRowSpan - 1) / kRowSpan);
         prefill_combine_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(
             y_d, (int)hidden, (int)T, (int)topk, ro.route_pos, ro.row_expert, down_svh, weights,
             w_dtype, out, out_dtype);

@@ -26,6 +26,7 @@ namespace exl3 {
 namespace {
 
 constexpr int kRouteWaves = kRouteThreads / 64;
+constexpr int kRouteBatch = 8;  // 64-route rows whose keys a wave loads at once
 
 // Exclusive prefix sum over the 1024 threads of the block; returns this
 // thread's prefix and writes the total to *total.  `tmp` holds 16 ints.
@@ -91,23 +92,35 @@ __global__ __launch_bounds__(kRouteThreads) void route_multisplit_kernel(
 
     // Phase 1: per-wave stable ranks; route_pos temporarily holds the rank
     // of each route within its wave's run of the same expert.
+    // The keys of kRouteBatch consecutive 64-route rows are loaded before
+    // the first is ranked, so a wave waits on one memory round trip per
+    // batch instead of one per 64 routes.
     const int per = (n_routes + kRouteWaves - 1) / kRouteWaves;
     const int r0 = w * per, r1 = min(n_routes, r0 + per);
     int* wcnt = cnt + w * digits;
-    for (int base = r0; base < r1; base += 64) {
-        const int r = base + lane;
-        if (r < r1) {
-            const int key = route_key(ids, ids_i64, r, live_routes, n_local);
-            const uint64_t peers = peer_mask(key, nbits);
-            const int leader = __ffsll((unsigned long long)peers) - 1;
-            const int below = __popcll(peers & ((1ull << lane) - 1ull));
-            int old = 0;
-            if (lane == leader) {
-                old = wcnt[key];
-                wcnt[key] = old + __popcll(peers);
+    for (int base = r0; base < r1; base += 64 * kRouteBatch) {
+        int key[kRouteBatch];
+#pragma unroll
+        for (int b = 0; b < kRouteBatch; ++b) {
+            const int r = base + 64 * b + lane;
+            key[b] = r < r1 ? route_key(ids, ids_i64, r, live_routes, n_local) : n_local;
+        }
+#pragma unroll
+        for (int b = 0; b < kRouteBatch; ++b) {
+            const int r = base + 64 * b + lane;
+            if (base + 64 * b >= r1) break;  // wave-uniform
+            if (r < r1) {
+                const uint64_t peers = peer_mask(key[b], nbits);
+                const int leader = __ffsll((unsigned long long)peers) - 1;
+                const int below = __popcll(peers & ((1ull << lane) - 1ull));
+                int old = 0;
+                if (lane == leader) {
+                    old = wcnt[key[b]];
+                    wcnt[key[b]] = old + __popcll(peers);
+                }
+                old = __shfl(old, leader, 64);
+                o.route_pos[r] = old + below;
             }
-            old = __shfl(old, leader, 64);
-            o.route_pos[r] = old + below;
         }
     }
     __syncthreads();
@@ -153,15 +166,26 @@ __global__ __launch_bounds__(kRouteThreads) void route_multisplit_kernel(
     __syncthreads();
 
     // Phase 3: sorted positions.
-    for (int r = r0 + lane; r < r1; r += 64) {
-        const int key = route_key(ids, ids_i64, r, live_routes, n_local);
-        if (key < n_local) {
-            const int pos = cnt[w * digits + key] + o.route_pos[r];
-            o.route_pos[r] = pos;
-            o.row_token[pos] = r / topk;
-            o.row_expert[pos] = key;
-        } else {
-            o.route_pos[r] = -1;
+    for (int base = r0; base < r1; base += 64 * kRouteBatch) {
+        int key[kRouteBatch], rank[kRouteBatch];
+#pragma unroll
+        for (int b = 0; b < kRouteBatch; ++b) {
+            const int r = base + 64 * b + lane;
+            key[b] = r < r1 ? route_key(ids, ids_i64, r, live_routes, n_local) : n_local;
+            rank[b] = r < r1 ? o.route_pos[r] : 0;
+        }
+#pragma unroll
+        for (int b = 0; b < kRouteBatch; ++b) {
+            const int r = base + 64 * b + lane;
+            if (r >= r1) continue;
+            if (key[b] < n_local) {
+                const int pos = cnt[w * digits + key[b]] + rank[b];
+                o.route_pos[r] = pos;
+                o.row_token[pos] = r / topk;
+                o.row_expert[pos] = key[b];
+            } else {
+                o.route_pos[r] = -1;
+            }
         }
     }
 }
