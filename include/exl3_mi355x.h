@@ -257,6 +257,30 @@ int exl3_nvfp4_sparse_decode(const void* q, int q_dtype, int64_t total_q, int64_
                              int64_t out_stride_n, int64_t out_stride_h, int64_t n_chunks,
                              void* workspace, int64_t workspace_bytes, void* stream);
 
+/* W1 write side of the NVFP4 pool: Gemma QK-norm + partial NeoX RoPE of the
+ * fused bf16 rows qkv [num_tokens][row_width] = [q | k | v | index_q |
+ * index_k] (128 dims per head; index heads only when num_index_heads > 0),
+ * then q -> q_out bf16 [T][num_heads][128]; K (normed, roped) and V (as is)
+ * -> q4 pack into slots 2h / 2h+1 of page slot_mapping[t] / 128, token
+ * slot_mapping[t] % 128 (negative or out-of-pool entries skip); index_q ->
+ * e4m3(bf16(v)) bytes into index_q_out [T][num_index_heads][128]; index_k ->
+ * e4m3(clamp(v, +-448)) into row index_slot_mapping[t] of index_cache
+ * [index_rows][128].  The processed K and index-K rows are written back into
+ * qkv.  Norm weights ([128], w_dtype) and cos_sin_cache ([max_positions]
+ * [rotary_dim] = cos | sin, cs_dtype): 0 fp16, 1 bf16, 2 fp32; rotary_dim a
+ * multiple of 8 up to 128.  A token whose position is outside
+ * [0, max_positions) is skipped.  Replaces q4_w1_insert + _q4_w1_kernel
+ * (src/vllm_exl3/minimax_q4kv_kernels.py:216-348, 661-758). */
+int exl3_nvfp4_w1_insert(void* qkv, int64_t num_tokens, int64_t row_width, const void* q_norm_w,
+                         const void* k_norm_w, const void* index_q_norm_w,
+                         const void* index_k_norm_w, int w_dtype, const void* cos_sin_cache,
+                         int cs_dtype, int64_t max_positions, const int64_t* positions,
+                         int64_t num_heads, int64_t num_kv_heads, int64_t num_index_heads,
+                         int64_t rotary_dim, float eps, const int64_t* slot_mapping,
+                         const int64_t* index_slot_mapping, void* pool, int64_t num_pages,
+                         void* index_cache, int64_t index_rows, void* q_out, void* index_q_out,
+                         void* stream);
+
 /* ---------------------------------------------------------------------------
  * Instrumentation (no counterpart in the reference; used by the benchmark to
  * time individual kernels on their launch stream).  Between begin and end,

@@ -256,3 +256,110 @@ def sparse_decode(q, kv_vals, topk_idx, block_table, seq_lens, decode_query_len:
             p /= p.sum(axis=1, keepdims=True)
             out[i, h * G:(h + 1) * G] = p @ V
     return out
+
+
+# ---------------------------------------------------------------------------
+# W1 write side: Gemma QK-norm + partial NeoX RoPE + q4 pack-insert
+# (``reference_w1_write``, ``minimax_q4kv_reference.py:422-612``)
+# ---------------------------------------------------------------------------
+
+def sumsq_tree(x) -> np.ndarray:
+    """Sum of squares over the last axis (128) in one fixed fp32 order:
+    adjacent pairs (2i, 2i+1) first, then a balanced tree over the 64 pair
+    sums in index order.  The reference reduces with ``torch.sum``, whose
+    order is unspecified; this order is the one the GPU kernel uses (a
+    butterfly over lanes that hold dims 2l, 2l+1), so the oracle pins the
+    kernel bit for bit and the reference within fp32 reduction rounding."""
+    x = np.asarray(x, dtype=np.float32)
+    sq = (x * x).astype(np.float32)
+    p = (sq[..., 0::2] + sq[..., 1::2]).astype(np.float32)
+    while p.shape[-1] > 1:
+        p = (p[..., 0::2] + p[..., 1::2]).astype(np.float32)
+    return p[..., 0]
+
+
+def gemma_rmsnorm(x, w, eps: float, sumsq=sumsq_tree) -> np.ndarray:
+    """``x * (1 / sqrt(mean(x^2) + eps)) * (1 + w)`` in fp32, each operation
+    rounded once, left to right (``gemma_rmsnorm``, ``:422-432``)."""
+    x = np.asarray(x, dtype=np.float32)
+    ss = sumsq(x).astype(np.float32)
+    d = (ss / np.float32(HEAD_DIM) + np.float32(eps)).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt(d).astype(np.float32)).astype(np.float32)
+    w1 = (np.float32(1.0) + np.asarray(w, dtype=np.float32)).astype(np.float32)
+    return ((x * r[..., None]).astype(np.float32) * w1).astype(np.float32)
+
+
+def rope_partial_neox(x, cos_sin_rows, rotary_dim: int) -> np.ndarray:
+    """Rotate the first ``rotary_dim`` dims of each 128-row: pairs (i, i+half)
+    as y[i] = x[i] c[i] - x[i+half] s[i], y[i+half] = x[i+half] c[i] +
+    x[i] s[i], the rest unchanged (``rope_partial_neox``, ``:435-464``).
+    ``cos_sin_rows`` [..., rotary_dim] = [cos | sin], broadcast over heads."""
+    x = np.asarray(x, dtype=np.float32)
+    half = rotary_dim // 2
+    d = np.arange(HEAD_DIM)
+    in_rope = d < rotary_dim
+    ci = np.where(d < half, d, d - half).clip(0, max(half - 1, 0))
+    partner = np.where(in_rope, np.where(d < half, d + half, d - half), d)
+    cs = np.asarray(cos_sin_rows, dtype=np.float32)
+    c = cs[..., ci]
+    s = cs[..., (ci + half).clip(0, rotary_dim - 1)]
+    while c.ndim < x.ndim:
+        c, s = c[..., None, :], s[..., None, :]
+    px = x[..., partner]
+    t1 = (x * c).astype(np.float32)
+    t2 = (px * s).astype(np.float32)
+    rot = np.where(d < half, t1 - t2, t1 + t2).astype(np.float32)
+    return np.where(in_rope, rot, x).astype(np.float32)
+
+
+def e4m3_clamped(x) -> np.ndarray:
+    """e4m3 bytes of clamp(x, +-448), NaN -> -448 (``_e4m3_clamped``,
+    ``:613-617``)."""
+    v = np.asarray(x, dtype=np.float32)
+    v = np.where(np.isnan(v), np.float32(-448.0), v)
+    return e4m3_encode(np.clip(v, -448.0, 448.0).astype(np.float32))
+
+
+def w1_write(qkv, q_norm_w, k_norm_w, iq_norm_w, ik_norm_w, cos_sin, positions, eps: float,
+             rotary_dim: int, nq: int, nkv: int, niq: int, slot_mapping, index_slot_mapping,
+             pool, index_cache, sumsq=sumsq_tree) -> dict:
+    """``reference_w1_write`` (``:467-578``) writing into existing buffers:
+    ``pool`` uint8 [pages, 2*nkv, 9216] and ``index_cache`` uint8 [rows, 128]
+    are updated in place at the mapped slots (-1 skips); returns q (bf16
+    values as float32), index_q bytes and the processed K / index-K rows
+    (bf16 values, the rows the reference kernel writes back into qkv)."""
+    x = np.asarray(qkv, dtype=np.float32).reshape(len(qkv), -1, HEAD_DIM)
+    T = x.shape[0]
+    cs = np.asarray(cos_sin, dtype=np.float32)[np.asarray(positions, dtype=np.int64)][:, :rotary_dim]
+
+    def proc(sl, w):
+        return rope_partial_neox(gemma_rmsnorm(sl, w, eps, sumsq), cs, rotary_dim)
+
+    q = bf16_round(proc(x[:, :nq], q_norm_w))
+    kn = bf16_round(proc(x[:, nq:nq + nkv], k_norm_w))
+    vb = bf16_round(x[:, nq + nkv:nq + 2 * nkv])
+    sm = np.asarray(slot_mapping, dtype=np.int64)
+    for i in range(T):
+        if sm[i] < 0:
+            continue
+        page, t = int(sm[i] // PAGE_TOKENS), int(sm[i] % PAGE_TOKENS)
+        for h in range(nkv):
+            for side, rows in ((0, kn), (1, vb)):
+                data, sc = pack_row(rows[i, h])
+                region = pool[page, 2 * h + side]
+                region[t * DATA_BYTES:(t + 1) * DATA_BYTES] = data
+                for g in range(NUM_GROUPS):
+                    region[DATA_REGION + scale_offset(side, t, g)] = sc[g]
+    out = {"q": q, "k_rows": kn}
+    if niq:
+        lo = nq + 2 * nkv
+        iq = proc(x[:, lo:lo + niq], iq_norm_w)
+        out["index_q"] = e4m3_encode(bf16_round(iq))
+        ik = proc(x[:, lo + niq], ik_norm_w)
+        out["ik_rows"] = bf16_round(ik)
+        kb = e4m3_clamped(ik)
+        ism = np.asarray(index_slot_mapping, dtype=np.int64)
+        for i in range(T):
+            if ism[i] >= 0:
+                index_cache[ism[i]] = kb[i]
+    return out

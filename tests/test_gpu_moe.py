@@ -239,3 +239,25 @@ def test_moe_config1_full_size(gpu, gemv_policy, T):
     got = _forward(dl, x, ids, w, E, I, 0)
     want = torch_moe_reference(x.float(), ids, w, dense, E)
     assert rel_l2(got, want) <= TOL
+
+
+def test_moe_from_checkpoint_packs(gpu):
+    # Packs named as the reference's checkpoints name them
+    # (experts.{e}.{w1,w3,w2}.{trellis,suh,svh,mcg}), loaded into pointer and
+    # K tables by vllm_exl3_amd.packs, then run through both executors.
+    from vllm_exl3_amd import packs as P
+
+    E, H, I, topk, T = 5, 256, 384, 3, 4
+    ks = [(2, 3, 4), (4, 2, 3), (3, 3, 3), (2, 2, 2), (4, 4, 4)]
+    experts = S.moe_layer(91, E, H, I, ks)
+    prefix = "model.layers.3.mlp.experts"
+    et = P.load_experts(P.state_dict_of(experts, prefix, P.CB_MCG), prefix, E, gpu)
+    x = S.activations(92, T, H)
+    ids, w = S.softmax_topk(93, T, E, topk)
+    want = O.moe_reference(x, ids, w, dense_cpu(experts, 1))
+    xd = torch.from_numpy(x).to(gpu).bfloat16()
+    idd, wd = torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu)
+    got = C.moe_forward(xd, idd, wd, et.tables, et.n_local, et.intermediate, **et.forward_kwargs())
+    assert rel_l2(got, want) <= TOL
+    got_p = C.moe_prefill(xd, idd, wd, et.tables, et.n_local, et.intermediate, **et.forward_kwargs())
+    assert rel_l2(got_p, want) <= TOL

@@ -140,3 +140,75 @@ def test_sparse_decode_graph_replay_and_errors(gpu):
         Q.q4_sparse_decode(qt[:, :, :64], pool, tkt, btt, st, 2, 0.1, out, 1)
     with pytest.raises(ValueError):
         Q.q4_sparse_decode(qt, pool.view(torch.int8), tkt, btt, st, 2, 0.1, out, 1)
+
+
+# ---------------------------------------------------------------------------
+# W1 write side: bit-exact against the oracle's norm/RoPE/pack restatement
+# (the oracle uses the kernel's fixed fp32 reduction order; it is pinned to
+# the closed forms and to the reference test's layout in test_oracle_nvfp4.py)
+# ---------------------------------------------------------------------------
+
+def _w1_case(gpu, seed, T, nq, nkv, niq, rot, n_pages, max_pos=4096, w_dtype=torch.float32):
+    g = np.random.default_rng(seed)
+    per = nq + 2 * nkv + (niq + 1 if niq else 0)
+    qkv = N.bf16_round((g.standard_normal((T, per * 128)) * 0.5).astype(np.float32))
+    ws = [N.bf16_round(g.standard_normal(128).astype(np.float32) * 0.5) for _ in range(4)]
+    inv = 1.0 / (5e6 ** (np.arange(0, rot, 2) / rot))
+    ang = np.outer(np.arange(max_pos), inv)
+    cs = np.concatenate([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+    pos = g.integers(0, max_pos, T).astype(np.int64)
+    sm = g.permutation(n_pages * 128)[:T].astype(np.int64)
+    sm[g.random(T) < 0.2] = -1
+    ism = g.permutation(2 * T)[:T].astype(np.int64)
+    ism[g.random(T) < 0.2] = -1
+    return qkv, ws, cs, pos, sm, ism
+
+
+@pytest.mark.parametrize("T, nq, nkv, niq, rot", [(5, 8, 4, 4, 64), (37, 6, 2, 0, 128),
+                                                  (300, 48, 8, 2, 64), (64, 4, 1, 1, 8)])
+def test_w1_insert_bit_exact(gpu, T, nq, nkv, niq, rot):
+    n_pages, eps = 4, 1e-6
+    qkv, ws, cs, pos, sm, ism = _w1_case(gpu, 100 + T, T, nq, nkv, niq, rot, n_pages)
+    pool = np.zeros((n_pages, 2 * nkv, N.SLOT_REGION), np.uint8)
+    icache = np.zeros((2 * T, 128), np.uint8)
+    want = N.w1_write(qkv, *ws, cs, pos, eps, rot, nq, nkv, niq, sm, ism, pool, icache)
+
+    d_qkv = torch.from_numpy(qkv).to(gpu).bfloat16()
+    d_w = [torch.from_numpy(w).to(gpu) for w in ws]
+    d_pool = Q.new_pool(n_pages, nkv, gpu)
+    d_ic = torch.zeros((2 * T, 128), dtype=torch.uint8, device=gpu)
+    q_out = torch.empty((T, nq * 128), dtype=torch.bfloat16, device=gpu)
+    iq_out = torch.empty((T, max(niq, 1) * 128), dtype=torch.uint8, device=gpu)[:, :niq * 128]
+    Q.q4_w1_insert(d_qkv, d_w[0], d_w[1], torch.from_numpy(cs).to(gpu), torch.from_numpy(pos).to(gpu),
+                   nq, nkv, rot, eps, d_w[2] if niq else None, d_w[3] if niq else None, niq,
+                   torch.from_numpy(sm).to(gpu), torch.from_numpy(ism).to(gpu), d_pool,
+                   d_ic if niq else None, 128, q_out, iq_out.contiguous() if niq else None)
+    torch.cuda.synchronize()
+    bits = lambda t: t.cpu().view(torch.int16).numpy()
+    wq = torch.from_numpy(want["q"].reshape(T, -1)).bfloat16()
+    assert np.array_equal(bits(q_out), bits(wq)), "q"
+    assert np.array_equal(_pool_bytes(d_pool), pool), "pool"
+    # processed K (and index-K) rows written back into qkv; other rows unchanged
+    back = torch.from_numpy(qkv).bfloat16().view(T, -1, 128).clone()
+    back[:, nq:nq + nkv] = torch.from_numpy(want["k_rows"]).bfloat16()
+    if niq:
+        back[:, -1] = torch.from_numpy(want["ik_rows"]).bfloat16()
+        assert np.array_equal(d_ic.cpu().numpy(), icache), "index_k"
+    assert np.array_equal(bits(d_qkv.view(T, -1, 128)), bits(back)), "qkv write-back"
+
+
+def test_w1_insert_matches_itself_in_index_q(gpu):
+    # index_q bytes: e4m3(bf16(v)) of the processed index_q rows
+    T, nq, nkv, niq, rot = 9, 2, 1, 3, 64
+    qkv, ws, cs, pos, sm, ism = _w1_case(gpu, 7, T, nq, nkv, niq, rot, 1)
+    pool = np.zeros((1, 2, N.SLOT_REGION), np.uint8)
+    icache = np.zeros((2 * T, 128), np.uint8)
+    want = N.w1_write(qkv, *ws, cs, pos, 1e-6, rot, nq, nkv, niq, sm, ism, pool, icache)
+    d_w = [torch.from_numpy(w).to(gpu) for w in ws]
+    iq_out = torch.zeros((T, niq * 128), dtype=torch.uint8, device=gpu)
+    Q.q4_w1_insert(torch.from_numpy(qkv).to(gpu).bfloat16(), d_w[0], d_w[1],
+                   torch.from_numpy(cs).to(gpu), torch.from_numpy(pos).to(gpu), nq, nkv, rot, 1e-6,
+                   d_w[2], d_w[3], niq, torch.from_numpy(sm).to(gpu), torch.from_numpy(ism).to(gpu),
+                   Q.new_pool(1, nkv, gpu), torch.zeros((2 * T, 128), dtype=torch.uint8, device=gpu),
+                   128, torch.empty((T, nq * 128), dtype=torch.bfloat16, device=gpu), iq_out)
+    assert np.array_equal(iq_out.cpu().numpy().reshape(T, niq, 128), want["index_q"])

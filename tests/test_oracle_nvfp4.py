@@ -12,6 +12,7 @@
 import pathlib
 
 import numpy as np
+import pytest
 import torch
 
 import nvfp4 as N
@@ -141,3 +142,96 @@ def test_pack_pages_places_tokens_and_sparse_attention_closed_form():
     # query 1 (seq 129, pos 128), head 1: blocks {0, 1}; block 1 holds one token
     want = np.concatenate([kv[1, 3, :128], kv[3, 3, :1]]).mean(axis=0)
     assert np.allclose(out[1, 2], want)
+
+
+# ---------------------------------------------------------------------------
+# W1 write side (Gemma norm + partial NeoX RoPE + q4 pack-insert)
+# ---------------------------------------------------------------------------
+
+W1_NQ, W1_NKV, W1_NIQ, W1_ROT = 8, 4, 4, 64  # the reference test's branch layout
+
+
+def w1_batch(num_tokens=5, seed=4):
+    """Inputs shaped like the reference's _w1_batch (tests/test_minimax_q4kv.py:
+    246-265): bf16 rows N(0, 0.25), N(0,1) norm weights and cos/sin rows,
+    positions 3.., slots [0, 1, 130, -1, 257]."""
+    g = np.random.default_rng(seed)
+    width = (W1_NQ + 2 * W1_NKV + W1_NIQ + 1) * 128
+    qkv = N.bf16_round((g.standard_normal((num_tokens, width)) * 0.5).astype(np.float32))
+    ws = [g.standard_normal(128).astype(np.float32) for _ in range(4)]
+    cos_sin = g.standard_normal((64, W1_ROT)).astype(np.float32)
+    positions = np.arange(num_tokens, dtype=np.int64) + 3
+    sm = np.array([0, 1, 130, -1, 257], dtype=np.int64)[:num_tokens]
+    ism = np.array([0, 1, 2, -1, 4], dtype=np.int64)[:num_tokens]
+    return qkv, ws, cos_sin, positions, 1e-4, sm, ism
+
+
+def test_w1_sumsq_tree_matches_float64():
+    x = np.random.default_rng(1).standard_normal((64, 128)).astype(np.float32)
+    want = (x.astype(np.float64) ** 2).sum(-1)
+    got = N.sumsq_tree(x).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 8 * np.finfo(np.float32).eps * want)
+    # a dropped or doubled term would be far outside that bound
+    assert N.sumsq_tree(np.ones((1, 128), np.float32))[0] == 128.0
+
+
+def test_w1_gemma_rmsnorm_closed_form():
+    g = np.random.default_rng(2)
+    x = g.standard_normal((32, 128)).astype(np.float32)
+    w = g.standard_normal(128).astype(np.float32)
+    eps = 1e-4
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + eps) * (1 + w.astype(np.float64))
+    got = N.gemma_rmsnorm(x, w, eps).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 1e-6 * np.abs(want) + 1e-7)
+    # w = 0 gives unit RMS (up to eps)
+    u = N.gemma_rmsnorm(x, np.zeros(128, np.float32), 0.0)
+    assert np.allclose(np.sqrt((u.astype(np.float64) ** 2).mean(-1)), 1.0, rtol=1e-6)
+
+
+@pytest.mark.parametrize("rot", [8, 64, 128])
+def test_w1_rope_is_complex_rotation(rot):
+    g = np.random.default_rng(3 + rot)
+    x = g.standard_normal((16, 128)).astype(np.float32)
+    th = g.uniform(-3, 3, (16, rot // 2))
+    cs = np.concatenate([np.cos(th), np.sin(th)], -1).astype(np.float32)
+    y = N.rope_partial_neox(x, cs, rot).astype(np.float64)
+    h = rot // 2
+    z = (x[:, :h] + 1j * x[:, h:rot]).astype(np.complex128) * (cs[:, :h] + 1j * cs[:, h:]).astype(np.complex128)
+    assert np.allclose(y[:, :h], z.real, rtol=0, atol=2e-6 * np.abs(x).max())
+    assert np.allclose(y[:, h:rot], z.imag, rtol=0, atol=2e-6 * np.abs(x).max())
+    assert np.array_equal(y[:, rot:], x[:, rot:].astype(np.float64))  # pass-through dims
+    # identity angle leaves the row unchanged bit for bit
+    ident = np.concatenate([np.ones((16, h)), np.zeros((16, h))], -1).astype(np.float32)
+    assert np.array_equal(N.rope_partial_neox(x, ident, rot), x)
+
+
+def test_w1_e4m3_clamped():
+    got = N.e4m3_clamped(np.array([np.nan, 1e9, -1e9, 448.0, 0.5, -0.0], np.float32))
+    assert got.tolist() == [0xFE, 0x7E, 0xFE, 0x7E, 0x30, 0x80]
+
+
+def test_w1_write_layout():
+    # Mirrors test_reference_w1_write_layout (tests/test_minimax_q4kv.py:268-330).
+    qkv, ws, cs, pos, eps, sm, ism = w1_batch()
+    pool = np.zeros((3, 2 * W1_NKV, N.SLOT_REGION), np.uint8)  # sm max 257 -> page 2
+    icache = np.zeros((5, 128), np.uint8)
+    out = N.w1_write(qkv, *ws, cs, pos, eps, W1_ROT, W1_NQ, W1_NKV, W1_NIQ, sm, ism, pool, icache)
+    assert out["q"].shape == (5, W1_NQ, 128) and out["index_q"].shape == (5, W1_NIQ, 128)
+    x = qkv.reshape(5, -1, 128)
+    csr = cs[pos]
+    kn = N.rope_partial_neox(N.gemma_rmsnorm(x[:, W1_NQ:W1_NQ + W1_NKV], ws[1], eps), csr, W1_ROT)
+    for i, s in enumerate(sm.tolist()):
+        if s < 0:
+            continue
+        page, tok = s // 128, s % 128
+        for h in range(W1_NKV):
+            got_k = N.unpack_slot(pool[page, 2 * h], 0)[tok]
+            got_v = N.unpack_slot(pool[page, 2 * h + 1], 1)[tok]
+            assert np.array_equal(got_k, N.unpack_row(*N.pack_row(kn[i, h])))
+            assert np.array_equal(got_v, N.unpack_row(*N.pack_row(x[i, W1_NQ + W1_NKV + h])))
+    # unmapped tokens leave the pool zero at their data positions
+    assert not pool[0, 0, 3 * 64:3 * 64 + 8].any()
+    assert not icache[3].any()
+    ikn = N.rope_partial_neox(N.gemma_rmsnorm(x[:, -1], ws[3], eps), csr, W1_ROT)
+    assert np.array_equal(icache[[0, 1, 2, 4]], N.e4m3_clamped(ikn)[[0, 1, 2, 4]])

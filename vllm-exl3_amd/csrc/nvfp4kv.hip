@@ -113,6 +113,32 @@ __device__ __forceinline__ int scale_offset(int side, int t, int g) {
     return ((t >> 2) * 4 + (g >> 1)) * 8 + (g & 1) * 4 + (t & 3);
 }
 
+// One 128-dim row held as dims 2 lane, 2 lane + 1 (bf16 values) packed into
+// token t of a slot region: data byte `lane` and, from every 8th lane, the
+// e4m3 scale of its 16-dim group.  Group max over 8 lanes, s = max(amax/6,
+// 2^-9) as saturating RNE e4m3, q = RZ(x * RN(1/s)), RNE e2m1 codes.
+__device__ __forceinline__ void pack_row_lane(float x0, float x1, uint8_t* region, int t, int side,
+                                              int lane) {
+    // amax ignores NaN (hardware fmax)
+    float am = fmaxf(x0 != x0 ? 0.0f : fabsf(x0), x1 != x1 ? 0.0f : fabsf(x1));
+    am = fmaxf(am, __shfl_xor(am, 1, 64));
+    am = fmaxf(am, __shfl_xor(am, 2, 64));
+    am = fmaxf(am, __shfl_xor(am, 4, 64));
+    const float s = fmaxf(am / 6.0f, 0.001953125f);  // 2^-9
+    const uint32_t sb = e4m3_encode(s);
+    const float recip = 1.0f / e4m3_value(sb);
+    uint32_t nib[2];
+    const float xs[2] = {x0, x1};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float q = rz_mul(xs[i], recip);
+        const uint32_t c = e2m1_code(fabsf(q));
+        nib[i] = c == 0 ? 0u : (c | ((__builtin_bit_cast(uint32_t, q) >> 31) << 3));
+    }
+    region[t * 64 + lane] = (uint8_t)(nib[0] | (nib[1] << 4));
+    if ((lane & 7) == 0) region[kQ4Data + scale_offset(side, t, lane >> 3)] = (uint8_t)sb;
+}
+
 struct Q4PackParams {
     const void* k;
     const void* v;
@@ -150,25 +176,139 @@ __global__ __launch_bounds__(256) void q4_pack_kernel(Q4PackParams p) {
         x0 = bf16_round(x0);
         x1 = bf16_round(x1);
     }
-    // group of 16 dims = 8 lanes; amax ignores NaN (hardware fmax)
-    float am = fmaxf(x0 != x0 ? 0.0f : fabsf(x0), x1 != x1 ? 0.0f : fabsf(x1));
-    am = fmaxf(am, __shfl_xor(am, 1, 64));
-    am = fmaxf(am, __shfl_xor(am, 2, 64));
-    am = fmaxf(am, __shfl_xor(am, 4, 64));
-    const float s = fmaxf(am / 6.0f, 0.001953125f);  // 2^-9
-    const uint32_t sb = e4m3_encode(s);
-    const float recip = 1.0f / e4m3_value(sb);
-    uint32_t nib[2];
-    const float xs[2] = {x0, x1};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float q = rz_mul(xs[i], recip);
-        const uint32_t c = e2m1_code(fabsf(q));
-        nib[i] = c == 0 ? 0u : (c | ((__builtin_bit_cast(uint32_t, q) >> 31) << 3));
-    }
     uint8_t* region = p.pool + (page * (2 * p.H) + 2 * h + side) * (int64_t)kQ4Slot;
-    region[t * 64 + lane] = (uint8_t)(nib[0] | (nib[1] << 4));
-    if ((lane & 7) == 0) region[kQ4Data + scale_offset(side, t, lane >> 3)] = (uint8_t)sb;
+    pack_row_lane(x0, x1, region, t, side, lane);
+}
+
+// ---------------------------------------------------------------------------
+// W1 write side: Gemma QK-norm + partial NeoX RoPE + q4 pack-insert
+// (q4_w1_insert / _q4_w1_kernel, src/vllm_exl3/minimax_q4kv_kernels.py:
+// 216-348, 661-758; reference reference_w1_write,
+// src/vllm_exl3/minimax_q4kv_reference.py:422-612).  One wave per (token,
+// branch head) of the fused bf16 row [q | k | v | index_q | index_k], lane l
+// holding dims 2l, 2l+1.  fp32 arithmetic with each operation rounded once
+// (no contraction): sum of squares as a butterfly over the lanes (pair sums,
+// then a balanced tree in lane order), r = 1/sqrt(ss/128 + eps) correctly
+// rounded, xn = (x r)(1 + w); RoPE pairs (d, d +- half) read their partner's
+// normed value from the owning lane.
+// ---------------------------------------------------------------------------
+struct Q4W1Params {
+    uint16_t* qkv;               // bf16 [T][row]; K and index-K rows rewritten in place
+    int64_t row;
+    uint16_t* q_out;             // bf16 [T][nq][128]
+    uint8_t* index_q_out;        // e4m3 bytes [T][niq][128]
+    const void* norm_w[4];       // q, k, index_q, index_k norm weights [128]
+    int w_dtype;
+    const void* cos_sin;         // [max_pos][rotary_dim] (cos | sin)
+    int cs_dtype;
+    int64_t max_pos;
+    const int64_t* positions;
+    const int64_t* slot_mapping;
+    const int64_t* index_slot_mapping;
+    uint8_t* pool;               // [pages][2 nkv][9216]
+    int64_t num_pages;
+    uint8_t* index_cache;        // e4m3 bytes [index_rows][128]
+    int64_t index_rows;
+    float eps;
+    int rotary_dim;
+    int T, nq, nkv, niq;
+};
+
+// fp32 product rounded on its own: the register barrier keeps the backend
+// from fusing it into a following add (one rounding, as a scalar CPU does).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+    float p = a * b;
+    asm volatile("" : "+v"(p));
+    return p;
+}
+
+__device__ __forceinline__ float w1_norm_rope(float& x0, float& x1, const void* w, int w_dtype,
+                                              const void* cs, int cs_dtype, int64_t pos,
+                                              int rotary_dim, float eps, int lane) {
+    float ss = mul_rn(x0, x0) + mul_rn(x1, x1);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss = ss + __shfl_xor(ss, m, 64);
+    // r = 1 / sqrt(ss / 128 + eps), the square root and the quotient each
+    // correctly rounded to fp32: both are taken in fp64 and rounded once to
+    // fp32, which gives the correctly rounded fp32 result (53 >= 2 * 24 + 2).
+    const float den = ss * 0.0078125f + eps;  // ss / 128 is exact
+    const float sq = (float)__builtin_sqrt((double)den);
+    const float r = (float)(1.0 / (double)sq);
+    const float n0 = mul_rn(mul_rn(x0, r), 1.0f + q4_load(w, w_dtype, 2 * lane));
+    const float n1 = mul_rn(mul_rn(x1, r), 1.0f + q4_load(w, w_dtype, 2 * lane + 1));
+    const int half = rotary_dim >> 1;
+    float y[2] = {n0, n1};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int d = 2 * lane + j;
+        const int pd = d < half ? d + half : (d < rotary_dim ? d - half : d);
+        const float a = __shfl(n0, pd >> 1, 64), b = __shfl(n1, pd >> 1, 64);  // every lane takes part
+        if (d < rotary_dim) {
+            const float pv = (pd & 1) ? b : a;
+            const int ci = d < half ? d : d - half;
+            const float c = q4_load(cs, cs_dtype, pos * rotary_dim + ci);
+            const float s = q4_load(cs, cs_dtype, pos * rotary_dim + half + ci);
+            const float t1 = mul_rn(y[j], c), t2 = mul_rn(pv, s);
+            y[j] = d < half ? t1 - t2 : t1 + t2;
+        }
+    }
+    x0 = y[0];
+    x1 = y[1];
+    return r;
+}
+
+__device__ __forceinline__ uint32_t bf16_bits(float v) { return __builtin_bit_cast(uint32_t, bf16_round(v)) >> 16; }
+
+__global__ __launch_bounds__(256) void q4_w1_kernel(Q4W1Params p) {
+    const int lane = threadIdx.x & 63;
+    const int per = p.nq + 2 * p.nkv + (p.niq > 0 ? p.niq + 1 : 0);
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= (int64_t)p.T * per) return;
+    const int64_t token = unit / per;
+    const int slot = (int)(unit % per);
+    const int64_t pos = p.positions[token];
+    if (pos < 0 || pos >= p.max_pos) return;  // wave-uniform; the host rejects these first
+    uint32_t* rowp = reinterpret_cast<uint32_t*>(p.qkv + token * p.row + (int64_t)slot * 128) + lane;
+    const uint32_t xw = *rowp;
+    float x0 = __builtin_bit_cast(float, xw << 16), x1 = __builtin_bit_cast(float, xw & 0xFFFF0000u);
+    const int iq_lo = p.nq + 2 * p.nkv;
+    if (slot < p.nq) {
+        w1_norm_rope(x0, x1, p.norm_w[0], p.w_dtype, p.cos_sin, p.cs_dtype, pos, p.rotary_dim, p.eps, lane);
+        reinterpret_cast<uint32_t*>(p.q_out + (token * p.nq + slot) * 128)[lane] =
+            bf16_bits(x0) | (bf16_bits(x1) << 16);
+    } else if (slot < p.nq + p.nkv) {
+        w1_norm_rope(x0, x1, p.norm_w[1], p.w_dtype, p.cos_sin, p.cs_dtype, pos, p.rotary_dim, p.eps, lane);
+        const float b0 = bf16_round(x0), b1 = bf16_round(x1);
+        *rowp = bf16_bits(x0) | (bf16_bits(x1) << 16);  // processed row back into qkv
+        const int64_t sm = p.slot_mapping[token];
+        if (sm >= 0 && sm < p.num_pages * kQ4Page) {
+            uint8_t* region = p.pool + ((sm / kQ4Page) * (2 * p.nkv) + 2 * (slot - p.nq)) * (int64_t)kQ4Slot;
+            pack_row_lane(b0, b1, region, (int)(sm % kQ4Page), 0, lane);
+        }
+    } else if (slot < iq_lo) {
+        const int64_t sm = p.slot_mapping[token];
+        if (sm >= 0 && sm < p.num_pages * kQ4Page) {
+            uint8_t* region =
+                p.pool + ((sm / kQ4Page) * (2 * p.nkv) + 2 * (slot - p.nq - p.nkv) + 1) * (int64_t)kQ4Slot;
+            pack_row_lane(x0, x1, region, (int)(sm % kQ4Page), 1, lane);  // bf16 inputs: values as is
+        }
+    } else if (slot < iq_lo + p.niq) {
+        w1_norm_rope(x0, x1, p.norm_w[2], p.w_dtype, p.cos_sin, p.cs_dtype, pos, p.rotary_dim, p.eps, lane);
+        const uint32_t e0 = e4m3_encode(bf16_round(x0)), e1 = e4m3_encode(bf16_round(x1));
+        reinterpret_cast<uint16_t*>(p.index_q_out + (token * p.niq + (slot - iq_lo)) * 128)[lane] =
+            (uint16_t)(e0 | (e1 << 8));
+    } else {
+        w1_norm_rope(x0, x1, p.norm_w[3], p.w_dtype, p.cos_sin, p.cs_dtype, pos, p.rotary_dim, p.eps, lane);
+        *rowp = bf16_bits(x0) | (bf16_bits(x1) << 16);
+        const int64_t ism = p.index_slot_mapping[token];
+        if (ism >= 0 && ism < p.index_rows) {
+            // e4m3(clamp(v, +-448)), NaN -> -448
+            const float c0 = x0 != x0 ? -448.0f : fminf(fmaxf(x0, -448.0f), 448.0f);
+            const float c1 = x1 != x1 ? -448.0f : fminf(fmaxf(x1, -448.0f), 448.0f);
+            reinterpret_cast<uint16_t*>(p.index_cache + ism * 128)[lane] =
+                (uint16_t)(e4m3_encode(c0) | (e4m3_encode(c1) << 8));
+        }
+    }
 }
 
 // Pool -> fp32 values [pages][2H][128][128]; one thread per data byte.
@@ -522,5 +662,67 @@ EXL3_API int exl3_nvfp4_sparse_decode(const void* q, int q_dtype, int64_t total_
                                                                out_stride_n, out_stride_h);
     EXL3_LAUNCHED();
     profile_mark(2, st);
+    return kOk;
+}
+
+EXL3_API int exl3_nvfp4_w1_insert(void* qkv, int64_t num_tokens, int64_t row_width,
+                                  const void* q_norm_w, const void* k_norm_w,
+                                  const void* index_q_norm_w, const void* index_k_norm_w,
+                                  int w_dtype, const void* cos_sin_cache, int cs_dtype,
+                                  int64_t max_positions, const int64_t* positions,
+                                  int64_t num_heads, int64_t num_kv_heads, int64_t num_index_heads,
+                                  int64_t rotary_dim, float eps, const int64_t* slot_mapping,
+                                  const int64_t* index_slot_mapping, void* pool, int64_t num_pages,
+                                  void* index_cache, int64_t index_rows, void* q_out,
+                                  void* index_q_out, void* stream) {
+    EXL3_CHECK(num_tokens >= 1, "q4 W1 requires a positive token count");
+    EXL3_CHECK(num_heads >= 1 && num_kv_heads >= 1 && num_index_heads >= 0,
+               "q4 W1 requires num_heads, num_kv_heads >= 1 and num_index_heads >= 0");
+    const int64_t per = num_heads + 2 * num_kv_heads + (num_index_heads > 0 ? num_index_heads + 1 : 0);
+    EXL3_CHECK(row_width == per * kQ4Dim, "q4 W1 qkv width %lld does not match the branch layout %lld",
+               (long long)row_width, (long long)(per * kQ4Dim));
+    EXL3_CHECK(rotary_dim > 0 && rotary_dim <= kQ4Dim && rotary_dim % 8 == 0,
+               "q4 W1 requires 0 < rotary_dim <= 128 and rotary_dim %% 8 == 0, got %lld",
+               (long long)rotary_dim);
+    EXL3_CHECK(w_dtype >= 0 && w_dtype <= 2 && cs_dtype >= 0 && cs_dtype <= 2,
+               "dtype ids: 0 fp16, 1 bf16, 2 fp32");
+    EXL3_CHECK(max_positions >= 1 && num_pages >= 1 && num_tokens * per < (1ll << 40),
+               "q4 W1: empty or oversized geometry");
+    EXL3_CHECK(qkv && q_norm_w && k_norm_w && cos_sin_cache && positions && slot_mapping && pool && q_out,
+               "null pointer argument");
+    EXL3_CHECK(num_index_heads == 0 ||
+                   (index_q_norm_w && index_k_norm_w && index_slot_mapping && index_cache &&
+                    index_q_out && index_rows >= 1),
+               "q4 W1 with index heads needs the index norm weights, slot mapping, cache and "
+               "index_q buffer");
+    Q4W1Params p = {};
+    p.qkv = reinterpret_cast<uint16_t*>(qkv);
+    p.row = row_width;
+    p.q_out = reinterpret_cast<uint16_t*>(q_out);
+    p.index_q_out = reinterpret_cast<uint8_t*>(index_q_out);
+    p.norm_w[0] = q_norm_w;
+    p.norm_w[1] = k_norm_w;
+    p.norm_w[2] = index_q_norm_w;
+    p.norm_w[3] = index_k_norm_w;
+    p.w_dtype = w_dtype;
+    p.cos_sin = cos_sin_cache;
+    p.cs_dtype = cs_dtype;
+    p.max_pos = max_positions;
+    p.positions = positions;
+    p.slot_mapping = slot_mapping;
+    p.index_slot_mapping = index_slot_mapping;
+    p.pool = reinterpret_cast<uint8_t*>(pool);
+    p.num_pages = num_pages;
+    p.index_cache = reinterpret_cast<uint8_t*>(index_cache);
+    p.index_rows = index_rows;
+    p.eps = eps;
+    p.rotary_dim = (int)rotary_dim;
+    p.T = (int)num_tokens;
+    p.nq = (int)num_heads;
+    p.nkv = (int)num_kv_heads;
+    p.niq = (int)num_index_heads;
+    const int64_t units = num_tokens * per;
+    q4_w1_kernel<<<(unsigned)((units + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(p);
+    EXL3_LAUNCHED();
     return kOk;
 }

@@ -138,3 +138,118 @@ def q4_sparse_decode(q: torch.Tensor, pool: torch.Tensor, topk_idx: torch.Tensor
                   sl.data_ptr(), int(decode_query_len), float(sm_scale), output.data_ptr(),
                   _DTYPE_ID[output.dtype], output.stride(0), output.stride(1), n_chunks,
                   ws.data_ptr(), ws.numel(), stream_of(dev))
+
+
+def _w1_vec(t: torch.Tensor | None, name: str, dev, n: int | None = None) -> None:
+    if t is None:
+        raise ValueError(f"q4 W1 refused: {name} is required")
+    if t.device != dev or not t.is_contiguous():
+        raise ValueError(f"q4 W1 refused: {name} must be a contiguous tensor on qkv's device")
+    if n is not None and t.numel() != n:
+        raise ValueError(f"q4 W1 refused: {name} must hold {n} values")
+
+
+def q4_w1_insert(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                 cos_sin_cache: torch.Tensor, positions: torch.Tensor, num_heads: int,
+                 num_kv_heads: int, rotary_dim: int, eps: float,
+                 index_q_norm_w: torch.Tensor | None, index_k_norm_w: torch.Tensor | None,
+                 num_index_heads: int, slot_mapping: torch.Tensor | None,
+                 index_slot_mapping: torch.Tensor | None, pool: torch.Tensor,
+                 index_cache: torch.Tensor | None, block_size: int, q_out: torch.Tensor | None,
+                 index_q_out: torch.Tensor | None, *, check_positions: bool | None = None) -> None:
+    """The W1 write path: Gemma QK-norm + partial NeoX RoPE of the fused bf16
+    rows ``qkv`` [T, (nq + 2 nkv [+ niq + 1]) * 128] = [q | k | v | index_q |
+    index_k], then: q -> ``q_out`` (bf16 [T, nq*128]); K and V -> q4 pack into
+    pool slots 2h / 2h+1 of page ``slot_mapping // 128`` (-1 skips); index_q
+    -> e4m3(bf16(v)) bytes into ``index_q_out``; index_k -> e4m3(clamp(v,
+    +-448)) into row ``index_slot_mapping`` of ``index_cache``.  The processed
+    K and index-K rows are written back into ``qkv`` (bf16), as the
+    reference kernel does.
+
+    Same arguments and refusal rules as ``q4_w1_insert``
+    (src/vllm_exl3/minimax_q4kv_kernels.py:661-758, validate_w1_call
+    src/vllm_exl3/minimax_q4kv_reference.py:625-732): bf16 rows, 128-token
+    blocks, rotary_dim % 8 == 0, fp8 e4m3 index buffers (float8_e4m3fn or
+    their uint8 byte views); refusals raise ``ValueError("q4 W1 refused:
+    ...")`` before any launch.  As in the reference, a ``slot_mapping`` (or
+    ``index_slot_mapping``) of None means ``positions`` serves as the slot
+    mapping.  ``check_positions`` (default: when the stream is not being
+    captured) verifies on the host that every position has a cos/sin row;
+    the kernel itself skips a token whose position has none."""
+    dev = qkv.device
+    errors = []
+    if qkv.dtype is not torch.bfloat16:
+        errors.append(f"q4 W1 requires bfloat16 qkv rows, got {qkv.dtype}")
+    niq = int(num_index_heads)
+    per = num_heads + 2 * num_kv_heads + (niq + 1 if niq > 0 else 0)
+    if qkv.dim() != 2 or qkv.size(1) != per * HEAD_DIM:
+        errors.append(f"q4 W1 qkv width {qkv.size(-1)} does not match the branch layout "
+                      f"{per * HEAD_DIM}")
+    if qkv.dim() == 2 and qkv.size(0) <= 0:
+        errors.append("q4 W1 requires a positive token count")
+    if not (0 < rotary_dim <= HEAD_DIM and rotary_dim % 8 == 0):
+        errors.append(f"q4 W1 requires 0 < rotary_dim <= 128 and rotary_dim % 8 == 0, "
+                      f"got {rotary_dim}")
+    if block_size != PAGE_TOKENS:
+        errors.append(f"q4 W1 requires block_size {PAGE_TOKENS}, got {block_size}")
+    if q_out is None:
+        errors.append("q4 W1 requires the bf16 q_out buffer")
+    fp8 = getattr(torch, "float8_e4m3fn", None)
+    for nm, t in (("index_cache", index_cache), ("index_q_out", index_q_out)):
+        if niq > 0 and t is not None and t.dtype not in (fp8, torch.uint8):
+            errors.append(f"q4 W1 requires the fp8 e4m3 {nm}, got {t.dtype}")
+    if errors:
+        raise ValueError("q4 W1 refused: " + "; ".join(errors))
+    _check_pool(pool, num_kv_heads)
+    if not qkv.is_cuda or not qkv.is_contiguous():
+        raise ValueError("q4 W1 refused: qkv must be a contiguous device tensor")
+    T = qkv.size(0)
+    if q_out.dtype is not torch.bfloat16 or q_out.numel() != T * num_heads * HEAD_DIM:
+        raise ValueError("q4 W1 refused: q_out must be bf16 [T, num_heads*128]")
+    _w1_vec(q_out, "q_out", dev)
+    _w1_vec(q_norm_w, "q_norm_w", dev, HEAD_DIM)
+    _w1_vec(k_norm_w, "k_norm_w", dev, HEAD_DIM)
+    if positions.dtype is not torch.int64:
+        raise ValueError("q4 W1 refused: positions must be int64")
+    _w1_vec(positions, "positions", dev, T)
+    sm = positions if slot_mapping is None else slot_mapping
+    ism = positions if index_slot_mapping is None else index_slot_mapping
+    for nm, t in (("slot_mapping", sm), ("index_slot_mapping", ism)):
+        if t.dtype is not torch.int64:
+            raise ValueError(f"q4 W1 refused: {nm} must be int64")
+        _w1_vec(t, nm, dev, T)
+    if cos_sin_cache.dim() != 2 or cos_sin_cache.size(1) != rotary_dim:
+        raise ValueError(f"q4 W1 refused: cos_sin_cache must be [rows, {rotary_dim}]")
+    _w1_vec(cos_sin_cache, "cos_sin_cache", dev)
+    dts = {q_norm_w.dtype, k_norm_w.dtype}
+    iqw = ikw = idx_q = idx_c = None
+    rows = 0
+    if niq > 0:
+        _w1_vec(index_q_norm_w, "index_q_norm_w", dev, HEAD_DIM)
+        _w1_vec(index_k_norm_w, "index_k_norm_w", dev, HEAD_DIM)
+        dts |= {index_q_norm_w.dtype, index_k_norm_w.dtype}
+        _w1_vec(index_q_out, "index_q_out", dev, T * niq * HEAD_DIM)
+        _w1_vec(index_cache, "index_cache", dev)
+        if index_cache.numel() % HEAD_DIM:
+            raise ValueError("q4 W1 refused: index_cache rows are 128 bytes")
+        rows = index_cache.numel() // HEAD_DIM
+        iqw, ikw = index_q_norm_w.data_ptr(), index_k_norm_w.data_ptr()
+        idx_q, idx_c = index_q_out.data_ptr(), index_cache.data_ptr()
+    if len(dts) != 1 or next(iter(dts)) not in _DTYPE_ID:
+        raise ValueError("q4 W1 refused: norm weights must share one of fp16/bf16/fp32")
+    if cos_sin_cache.dtype not in _DTYPE_ID:
+        raise ValueError("q4 W1 refused: cos_sin_cache must be fp16/bf16/fp32")
+    if check_positions is None:
+        check_positions = not torch.cuda.is_current_stream_capturing()
+    if check_positions:
+        lo, hi = int(positions.min()), int(positions.max())
+        if lo < 0 or hi >= cos_sin_cache.size(0):
+            raise ValueError(f"positions [{lo}, {hi}] exceed the cos_sin_cache "
+                             f"({cos_sin_cache.size(0)} rows)")
+    with torch.cuda.device(dev):
+        _lib.call("exl3_nvfp4_w1_insert", qkv.data_ptr(), T, qkv.size(1), q_norm_w.data_ptr(),
+                  k_norm_w.data_ptr(), iqw, ikw, _DTYPE_ID[q_norm_w.dtype],
+                  cos_sin_cache.data_ptr(), _DTYPE_ID[cos_sin_cache.dtype], cos_sin_cache.size(0),
+                  positions.data_ptr(), num_heads, num_kv_heads, niq, rotary_dim, float(eps),
+                  sm.data_ptr(), ism.data_ptr(), pool.data_ptr(), pool.size(0), idx_c, rows,
+                  q_out.data_ptr(), idx_q, stream_of(dev))
