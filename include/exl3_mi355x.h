@@ -257,6 +257,18 @@ int exl3_nvfp4_sparse_decode(const void* q, int q_dtype, int64_t total_q, int64_
                              int64_t out_stride_n, int64_t out_stride_h, int64_t n_chunks,
                              void* workspace, int64_t workspace_bytes, void* stream);
 
+/* n-gram embedding rows: packed int16 [n_rows][row_stride] (word 0 an fp16
+ * scale, then 160 K-bit ring values, K = bits in 1..8, row_stride >=
+ * 1 + 10 * bits), heads int64 [n_rows], head_bias fp16 [num_heads][160] ->
+ * out fp16 [n_rows][160] = fp16(mul1(state_i) * scale + head_bias[head]),
+ * state_i's K-bit groups j = ring values (i - j) mod 160.  A head outside
+ * [0, num_heads) contributes a zero bias.  Replaces exllamav3_ext's
+ * ngram_dequant, whose pure-torch twin is ngram_dequant_rows_torch
+ * (src/vllm_exl3/exl3.py:5170-5238). */
+int exl3_ngram_dequant(const int16_t* packed, int64_t n_rows, int64_t row_stride, int bits,
+                       const int64_t* heads, const uint16_t* head_bias, int64_t num_heads,
+                       uint16_t* out, void* stream);
+
 /* W1 write side of the NVFP4 pool: Gemma QK-norm + partial NeoX RoPE of the
  * fused bf16 rows qkv [num_tokens][row_width] = [q | k | v | index_q |
  * index_k] (128 dims per head; index heads only when num_index_heads > 0),

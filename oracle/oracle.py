@@ -444,3 +444,40 @@ def attention_decode_lens(q: np.ndarray, k: np.ndarray, v: np.ndarray, seq_lens:
         if n > 0:
             out[b:b + 1] = attention_decode(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n], scale)
     return out
+
+
+# ---------------------------------------------------------------------------
+# n-gram embedding rows (mul1 codebook, 160-dim ring bitstream)
+# ---------------------------------------------------------------------------
+NGRAM_ROW_DIM = 160
+
+
+def ngram_words_per_row(bits: int) -> int:
+    """One fp16 scale word plus the K-bit ring bitstream (``exl3.py:5174-5176``)."""
+    return 1 + NGRAM_ROW_DIM * int(bits) // 16
+
+
+def ngram_bit_tables(bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """(word, bit) of state bit m of element i: ring position
+    ((i - m // K) mod 160) * K + m % K, one word after the scale
+    (``_ngram_bit_tables``, ``exl3.py:5196-5207``)."""
+    i = np.arange(NGRAM_ROW_DIM)[:, None]
+    m = np.arange(16)[None, :]
+    sb = ((i - m // bits) % NGRAM_ROW_DIM) * bits + m % bits
+    return 1 + (sb >> 4), sb & 15
+
+
+def ngram_dequant_rows(packed: np.ndarray, bits: int, heads: np.ndarray,
+                       head_bias: np.ndarray) -> np.ndarray:
+    """fp16 [N, 160] = fp16(codebook_mul1[state] * scale + head_bias[head]),
+    the product and the sum in fp32 (``ngram_dequant_rows_torch``,
+    ``exl3.py:5212-5238``)."""
+    packed = np.asarray(packed, dtype=np.int16)
+    widx, bidx = ngram_bit_tables(bits)
+    words = packed.astype(np.int64) & 0xFFFF
+    state = (((words[:, widx] >> bidx) & 1) << np.arange(16)).sum(-1)
+    cb = decode_codebook_table(2).view(np.float16)
+    vals = cb[state].astype(np.float32)
+    scale = packed[:, :1].copy().view(np.float16).astype(np.float32)
+    bias = np.asarray(head_bias, dtype=np.float16)[np.asarray(heads, dtype=np.int64)].astype(np.float32)
+    return ((vals * scale).astype(np.float32) + bias).astype(np.float16)

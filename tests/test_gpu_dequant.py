@@ -73,3 +73,17 @@ def test_dequant_rejects_bad_arguments(gpu, bad, match):
         su = su[:64]
     with pytest.raises(RuntimeError, match=match):
         C.dequant_trellis(t, su, sv, K, True)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_ngram_rows_bit_exact(gpu, bits):
+    g = np.random.default_rng(40 + bits)
+    n, words = 257, O.ngram_words_per_row(bits)
+    packed = g.integers(-32768, 32768, (n, words + 3)).astype(np.int16)  # padded row stride
+    packed[:, 0] = g.uniform(-2, 2, n).astype(np.float16).view(np.int16)
+    hb = g.standard_normal((5, 160)).astype(np.float16)
+    heads = g.integers(0, 5, n)
+    want = O.ngram_dequant_rows(packed[:, :words], bits, heads, hb)
+    got = C.ngram_dequant_rows(torch.from_numpy(packed).to(gpu)[:, :], bits,
+                               torch.from_numpy(heads).to(gpu), torch.from_numpy(hb).to(gpu))
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))

@@ -184,3 +184,58 @@ def test_dequant_constant_tile_is_single_spike():
     c = float(np.array([O.decode_codebook(0, 1)], dtype=np.uint16).view(np.float16)[0])
     assert np.count_nonzero(w) == 1
     assert w[0, 0] == pytest.approx(c * 128.0 * 128.0 / 128.0, rel=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# n-gram embedding rows (mul1 ring bitstream)
+# ---------------------------------------------------------------------------
+
+def _ring_pack(vals: np.ndarray, bits: int, scale: float) -> np.ndarray:
+    """Packed row from 160 K-bit ring values: value p occupies stream bits
+    [p K, p K + K), LSB-first in the int16 words after the fp16 scale word."""
+    n_words = O.ngram_words_per_row(bits)
+    stream = np.zeros(16 * (n_words - 1), np.uint8)
+    for p, v in enumerate(vals):
+        for b in range(bits):
+            stream[p * bits + b] = (int(v) >> b) & 1
+    words = (stream.reshape(-1, 16).astype(np.uint32) << np.arange(16)).sum(-1)
+    row = np.zeros(n_words, np.uint16)
+    row[0] = np.float16(scale).view(np.uint16)
+    row[1:] = words
+    return row.view(np.int16)
+
+
+def test_ngram_words_per_row_reference_vectors():
+    # tests/test_native_pack_unit.py:27-29 of the reference
+    assert O.ngram_words_per_row(5) == 51 and O.ngram_words_per_row(3) == 31
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 8])
+def test_ngram_state_is_the_ring_of_k_bit_values(bits):
+    g = np.random.default_rng(bits)
+    vals = g.integers(0, 1 << bits, 160)
+    row = _ring_pack(vals, bits, 1.0)
+    out = O.ngram_dequant_rows(row[None], bits, np.zeros(1, np.int64), np.zeros((1, 160), np.float16))
+    # state of element i: K-bit group j holds ring value (i - j) mod 160
+    groups = (16 + bits - 1) // bits
+    for i in (0, 1, 7, 80, 159):
+        st = 0
+        for j in range(groups):
+            st |= int(vals[(i - j) % 160]) << (j * bits)
+        st &= 0xFFFF
+        assert out[0, i].view(np.uint16) == O.decode_codebook(st, 2)
+
+
+def test_ngram_scale_and_bias():
+    g = np.random.default_rng(11)
+    bits = 4
+    rows = np.stack([_ring_pack(g.integers(0, 16, 160), bits, s) for s in (0.5, -4.0, 0.0078125)])
+    hb = g.standard_normal((3, 160)).astype(np.float16)
+    heads = np.array([2, 0, 1])
+    got = O.ngram_dequant_rows(rows, bits, heads, hb).astype(np.float64)
+    base = O.ngram_dequant_rows(rows, bits, np.zeros(3, np.int64), np.zeros((1, 160), np.float16))
+    scales = np.array([0.5, -4.0, 0.0078125])[:, None]
+    # base = fp16(cb * scale): exact in fp16 for power-of-two scales
+    cb = base.astype(np.float64) / scales
+    want = cb * scales + hb[heads].astype(np.float64)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -10 + 2.0 ** -24)

@@ -154,6 +154,54 @@ __global__ __launch_bounds__(256) void decode_tiles_kernel(const uint32_t* __res
         half_to_bits(decode_weight<CB>(win));
 }
 
+// ---------------------------------------------------------------------------
+// n-gram embedding rows (ngram_dequant; pure-torch twin
+// ngram_dequant_rows_torch, src/vllm_exl3/exl3.py:5170-5238): a packed row is
+// one fp16 scale word plus a ring bitstream of 160 K-bit values (LSB-first
+// in int16 words).  Element i's 16-bit mul1 state holds ring values i, i-1,
+// i-2, ... (mod 160) in its K-bit groups 0, 1, 2, ...; the value is
+// fp16(codebook(state) * scale + head_bias[head]).  One wave per row: the
+// row's words are staged in LDS, lane l decodes elements l, l + 64, l + 128.
+// ---------------------------------------------------------------------------
+constexpr int kNgramDim = 160;
+constexpr int kNgramMaxWords = 1 + kNgramDim * 8 / 16;  // K <= 8
+
+__global__ __launch_bounds__(256) void ngram_kernel(const int16_t* __restrict__ packed, int64_t n_rows,
+                                                   int64_t row_stride, int bits,
+                                                   const int64_t* __restrict__ heads,
+                                                   const uint16_t* __restrict__ head_bias,
+                                                   int64_t num_heads, uint16_t* __restrict__ out) {
+    __shared__ uint32_t lds[4][kNgramMaxWords + 1];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t row = (int64_t)blockIdx.x * 4 + w;
+    if (row >= n_rows) return;  // wave-uniform
+    const int words = 1 + kNgramDim * bits / 16;
+    const int16_t* src = packed + row * row_stride;
+    for (int j = lane; j < words; j += 64) lds[w][j] = (uint16_t)src[j];
+    if (lane == 0) lds[w][words] = 0;  // a 2-word read at the last word stays defined
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const float scale = (float)bits_to_half(lds[w][0]);
+    const int64_t head = heads[row];
+    const bool hok = head >= 0 && head < num_heads;
+    const int groups = (16 + bits - 1) / bits;
+    const uint32_t kmask = (1u << bits) - 1u;
+    for (int i = lane; i < kNgramDim; i += 64) {
+        uint32_t state = 0;
+        for (int j = 0; j < groups; ++j) {
+            int p = i - j;
+            if (p < 0) p += kNgramDim;
+            const int sb = p * bits;                 // first stream bit of ring value p
+            const int wi = 1 + (sb >> 4), bi = sb & 15;
+            const uint32_t two = lds[w][wi] | (lds[w][wi + 1] << 16);
+            state |= ((two >> bi) & kmask) << (j * bits);
+        }
+        const float v = (float)decode_weight<kCbMul1>(state & 0xFFFFu);
+        const float b = hok ? (float)bits_to_half(head_bias[head * kNgramDim + i]) : 0.0f;
+        out[row * kNgramDim + i] = half_to_bits(f32_to_f16_rne(v * scale + b));
+    }
+}
+
 }  // namespace
 }  // namespace exl3
 
@@ -213,6 +261,21 @@ EXL3_API int exl3_decode_tiles(const int16_t* trellis, int64_t tiles_k, int64_t 
         case 1: decode_tiles_kernel<1><<<nt, 256, 0, s>>>(t32, (int)tiles_n, (int)K, nt, out); break;
         default: decode_tiles_kernel<2><<<nt, 256, 0, s>>>(t32, (int)tiles_n, (int)K, nt, out); break;
     }
+    EXL3_LAUNCHED();
+    return kOk;
+}
+
+EXL3_API int exl3_ngram_dequant(const int16_t* packed, int64_t n_rows, int64_t row_stride, int bits,
+                                const int64_t* heads, const uint16_t* head_bias, int64_t num_heads,
+                                uint16_t* out, void* stream) {
+    EXL3_CHECK(bits >= 1 && bits <= 8, "ngram_dequant supports 1 <= bits <= 8, got %d", bits);
+    EXL3_CHECK(n_rows >= 0 && num_heads >= 1, "ngram_dequant: bad row or head count");
+    EXL3_CHECK(row_stride >= 1 + kNgramDim * bits / 16, "ngram_dequant: rows need %d words",
+               1 + kNgramDim * bits / 16);
+    if (n_rows == 0) return kOk;
+    EXL3_CHECK(packed && heads && head_bias && out, "null pointer argument");
+    ngram_kernel<<<(unsigned)((n_rows + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        packed, n_rows, row_stride, bits, heads, head_bias, num_heads, out);
     EXL3_LAUNCHED();
     return kOk;
 }

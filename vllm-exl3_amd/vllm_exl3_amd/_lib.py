@@ -56,6 +56,7 @@ SIGNATURES: dict[str, list] = {
     "exl3_nvfp4_sparse_decode": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64,
                                  _i64, _p, _i64, _i64, _p, _i64, _f32, _p, _i32, _i64, _i64, _i64,
                                  _p, _i64, _p],
+    "exl3_ngram_dequant": [_p, _i64, _i64, _i32, _p, _p, _i64, _p, _p],
     "exl3_nvfp4_w1_insert": [_p, _i64, _i64, _p, _p, _p, _p, _i32, _p, _i32, _i64, _p, _i64, _i64,
                              _i64, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _p, _p, _p],
     "exl3_profile_begin": [_i32],

@@ -538,3 +538,42 @@ def p2b_fused_moe_padded(x: torch.Tensor, out: torch.Tensor, gate_trellis_ptrs, 
                 int(n_local), intermediate_size, k_tables=(k_gate_tbl, k_up_tbl, k_down_tbl),
                 codebook=cb, swiglu_limit=swiglu_limit, n_valid=n_valid, out=out)
     return out
+
+
+NGRAM_ROW_DIM = 160
+
+
+def ngram_words_per_row(bits: int) -> int:
+    """Packed int16 words per n-gram row: one fp16 scale word plus the K-bit
+    ring bitstream (src/vllm_exl3/exl3.py:5174-5176)."""
+    return 1 + NGRAM_ROW_DIM * int(bits) // 16
+
+
+def ngram_dequant_rows(packed: torch.Tensor, bits: int, heads: torch.Tensor,
+                       head_bias: torch.Tensor, chunk: int = 8192) -> torch.Tensor:
+    """n-gram embedding rows on the GPU: packed int16 (N, words), heads (N,)
+    int, head_bias (num_heads, 160) fp16 -> (N, 160) fp16 =
+    codebook_mul1[state] * scale + head_bias[head] (the contract of
+    ngram_dequant_rows_torch, src/vllm_exl3/exl3.py:5212-5238; ``chunk`` is
+    accepted for signature compatibility, one launch covers all rows).
+    Heads outside [0, num_heads) contribute a zero bias."""
+    del chunk
+    _check(packed.dim() == 2 and packed.dtype == torch.int16 and packed.is_cuda
+           and packed.stride(1) == 1, "ngram_dequant needs packed int16 (N, words) rows on the GPU")
+    _check(1 <= int(bits) <= 8, "ngram_dequant supports 1 <= bits <= 8")
+    _check(packed.size(1) >= ngram_words_per_row(bits),
+           f"ngram rows need {ngram_words_per_row(bits)} words at {bits} bits")
+    dev = packed.device
+    n = packed.size(0)
+    _check(heads.dim() == 1 and heads.numel() == n and heads.device == dev,
+           "ngram_dequant heads must be one id per row on the rows' device")
+    _check(head_bias.dim() == 2 and head_bias.size(1) == NGRAM_ROW_DIM and head_bias.device == dev,
+           "ngram_dequant head_bias must be (num_heads, 160) on the rows' device")
+    h = heads.to(torch.int64).contiguous()
+    hb = head_bias.to(torch.float16).contiguous()
+    out = torch.empty((n, NGRAM_ROW_DIM), dtype=torch.float16, device=dev)
+    if n:
+        with torch.cuda.device(dev):
+            _lib.call("exl3_ngram_dequant", packed.data_ptr(), n, packed.stride(0), int(bits),
+                      h.data_ptr(), hb.data_ptr(), hb.size(0), out.data_ptr(), stream_of(dev))
+    return out
