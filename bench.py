@@ -319,7 +319,37 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
+    ap.add_argument("--fat-probe", default="", metavar="M,K,N",
+                    help="only run the fat GEMM (K4 MCG) on one dense M x K x N problem with "
+                         "host-generated inputs, 5 launches, and exit (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
+    if args.fat_probe:
+        import numpy as np
+        import torch
+
+        sys.path.insert(0, str(ROOT / "vllm-exl3_amd"))
+        from vllm_exl3_amd import synthetic as S
+        from vllm_exl3_amd import vllm_exl3_c as C
+
+        M, Kd, N = (int(v) for v in args.fat_probe.split(","))
+        lin = S.linear(7, Kd, N, 4)
+        dev = torch.device("cuda", 0)
+        a = torch.from_numpy(S.activations(8, M, Kd)).to(dev).half()
+        t = torch.from_numpy(lin["trellis"]).to(dev)
+        sv = torch.from_numpy(lin["svh"]).to(dev)
+        out = torch.empty((M, N), dtype=torch.float32, device=dev)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        C.exl3_fat_gemm(a, t, out, sv, 4, True, False)
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(5):
+            C.exl3_fat_gemm(a, t, out, sv, 4, True, False)
+        ev[1].record()
+        torch.cuda.synchronize()
+        us = ev[0].elapsed_time(ev[1]) / 5 * 1e3
+        print(json.dumps({"fat_probe": [M, Kd, N], "launches": 6, "us_per_launch": round(us, 2),
+                          "tflops": round(2 * M * Kd * N / us / 1e6, 1)}), flush=True)
+        return 0
     if args.copy_probe:
         import torch
 
