@@ -197,7 +197,7 @@ def test_w1_insert_bit_exact(gpu, T, nq, nkv, niq, rot):
     assert np.array_equal(bits(d_qkv.view(T, -1, 128)), bits(back)), "qkv write-back"
 
 
-def test_w1_insert_matches_itself_in_index_q(gpu):
+def test_w1_insert_index_q_bytes(gpu):
     # index_q bytes: e4m3(bf16(v)) of the processed index_q rows
     T, nq, nkv, niq, rot = 9, 2, 1, 3, 64
     qkv, ws, cs, pos, sm, ism = _w1_case(gpu, 7, T, nq, nkv, niq, rot, 1)
