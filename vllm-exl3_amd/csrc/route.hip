@@ -40,14 +40,16 @@ __device__ int block_exclusive_scan(int v, int* tmp, int* total) {
     }
     if (lane == 63) tmp[w] = incl;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        for (int i = 0; i < kRouteWaves; ++i) {
-            const int t = tmp[i];
-            tmp[i] = acc;
-            acc += t;
+    if (w == 0) {  // scan of the wave totals by one wave (shuffles, no serial loop)
+        const int t = lane < kRouteWaves ? tmp[lane] : 0;
+        int acc = t;
+#pragma unroll
+        for (int d = 1; d < kRouteWaves; d <<= 1) {
+            const int u = __shfl_up(acc, d, 64);
+            if (lane >= d) acc += u;
         }
-        tmp[kRouteWaves] = acc;
+        if (lane < kRouteWaves) tmp[lane] = acc - t;
+        if (lane == kRouteWaves - 1) tmp[kRouteWaves] = acc;
     }
     __syncthreads();
     const int r = tmp[w] + incl - v;
