@@ -311,6 +311,14 @@ int exl3_nvfp4_w1_insert(void* qkv, int64_t num_tokens, int64_t row_width, const
 int exl3_profile_begin(int max_calls);
 int exl3_profile_end(double* phase_ms, int max_phases, int* n_calls, int* n_phases);
 
+/* ---------------------------------------------------------------------------
+ * Seeded synthetic bits: dst[i] = high 32 bits of the SplitMix64 finaliser of
+ * seed + (i + 1) * 0x9E3779B97F4A7C15, i < n_words.  Deterministic across
+ * devices and launch shapes.  No counterpart in the reference: it generates
+ * the benchmark's and the full-size tests' synthetic weights and caches on
+ * the device without a library RNG kernel. */
+int exl3_fill_hash_u32(uint32_t* dst, int64_t n_words, uint64_t seed, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,8 +41,15 @@ ORACLE_PINS = {
     "hadamard": "vs oracle/_ref (bit-exact); H.H = 128 I; float64 matrix form",
     "dequant": "composition: float64 diag(suh) H Wq H diag(svh)/128 within one fp16 ulp; "
                "suh=svh=1 round trip; constant tile gives one non-zero per block",
-    "moe_loop": "reference activation vectors tests/test_activation_parity.py:46-53; "
-                "single-expert reduction to gemv; routing exact-sum stub",
+    "moe_loop": "tests/test_oracle_moe.py: the reference's activation vectors "
+                "(tests/test_activation_parity.py:46-81: 400.0, 99.9954605, five clamp "
+                "boundaries, non-positive limits); SwiGLU-OAI and relu2 closed forms; a "
+                "single-expert weight-1 reduction vs an independent torch float64 formula at "
+                "both rounding-point settings; an exact-sum routing case after "
+                "tests/test_routing_parity.py:84-111 with sentinels and an expert map; "
+                "planted clamp/activation mistakes fail these checks",
+    "map_topk_to_local": "tests/test_oracle_moe.py: exl3.py:2332-2354 cases (no map, map with "
+                         "negative / out-of-range entries, ids past the map)",
     "kv_int4": "closed form + brute force on tiny pages (format defined in-repo)",
     "attention": "float64 textbook softmax attention; uniform-key closed form",
 }
@@ -201,10 +208,23 @@ def gemv(x: np.ndarray, w16: np.ndarray) -> np.ndarray:
     return xf @ np.asarray(w16, dtype=np.float32)
 
 
-def map_topk_to_local(ids: np.ndarray, n_local: int) -> np.ndarray:
-    """Invalid ids -> n_local sentinel.  exl3.py:2330-2341 (no expert map)."""
+def map_topk_to_local(ids: np.ndarray, n_local: int,
+                      expert_map: np.ndarray | None = None) -> np.ndarray:
+    """Global expert ids -> local ids; invalid or non-local ids -> the
+    ``n_local`` sentinel.  src/vllm_exl3/exl3.py:2332-2354: without a map an
+    id is local when 0 <= id < n_local; with a map, ``expert_map[id]`` is the
+    local id (negative = not on this rank), valid when 0 <= id < len(map) and
+    0 <= map[id] < n_local."""
     ids = np.asarray(ids, dtype=np.int64)
-    return np.where((ids < 0) | (ids >= n_local), n_local, ids)
+    if expert_map is None:
+        return np.where((ids < 0) | (ids >= n_local), n_local, ids)
+    emap = np.asarray(expert_map, dtype=np.int64).reshape(-1)
+    n_global = emap.size
+    if n_global == 0:
+        return np.full_like(ids, n_local)
+    mapped = emap[np.clip(ids, 0, n_global - 1)]
+    invalid = (ids < 0) | (ids >= n_global) | (mapped < 0) | (mapped >= n_local)
+    return np.where(invalid, n_local, mapped)
 
 
 def silu(x: np.ndarray) -> np.ndarray:
@@ -212,24 +232,72 @@ def silu(x: np.ndarray) -> np.ndarray:
     return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
 
 
+def moe_activation(g: np.ndarray | None, u: np.ndarray, act: str = "silu",
+                   limit: float | None = None) -> np.ndarray:
+    """The routed expert's activation in fp32, with the reference's clamp rules.
+
+    src/vllm_exl3/exl3.py:2386-2410 (the eager loop) and csrc/p2b_moe.cu:
+    755-768 (the kernel): a limit > 0 clamps the gate from above only and the
+    up projection symmetrically; a limit of None, 0 or below is plain.
+    * ``silu``: silu(g) * u;
+    * ``swiglu_oai``: (u + 1) * g * sigmoid(1.702 g) (alpha 1.702, beta 1);
+    * gateless (``g is None``): relu(u)^2 with the symmetric up clamp."""
+    u = np.asarray(u, dtype=np.float32)
+    clamp = limit is not None and limit > 0
+    if g is None:
+        if clamp:
+            u = np.clip(u, np.float32(-limit), np.float32(limit))
+        return np.square(np.maximum(u, np.float32(0))).astype(np.float32)
+    g = np.asarray(g, dtype=np.float32)
+    if clamp:
+        g = np.minimum(g, np.float32(limit))
+        u = np.clip(u, np.float32(-limit), np.float32(limit))
+    if act == "swiglu_oai":
+        sig = np.float32(1.0) / (np.float32(1.0) + np.exp(np.float32(-1.702) * g))
+        return ((u + np.float32(1.0)) * g * sig).astype(np.float32)
+    if act != "silu":
+        raise ValueError(f"unknown activation {act!r}")
+    return (silu(g) * u).astype(np.float32)
+
+
+def _f16(a: np.ndarray) -> np.ndarray:
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
 def moe_reference(x: np.ndarray, ids: np.ndarray, weights: np.ndarray,
                   experts: list[dict], limit: float | None = None,
-                  act: str = "silu", round_down: bool = False) -> np.ndarray:
-    """Per-expert eager loop, fp32 accumulation.
+                  act: str = "silu", round_down: bool = False, gu_fp16: bool = True,
+                  expert_map: np.ndarray | None = None) -> np.ndarray:
+    """Per-route expert loop with fp32 accumulation: out[t] = sum over k of
+    w[t,k] * down(act(gate(x_t), up(x_t))) for the local experts of row t.
 
-    ``experts[e]`` holds dense fp16 matrices ``gate`` [H, I] (or None for a
-    gateless layer), ``up`` [H, I], ``down`` [I, H] as produced by
-    ``dequant``.  Rounding points follow exl3.py:2357-2413 and
-    tests/test_native_moe_contract.py:100-115: g and u rounded to fp16,
-    clamp (gate from above, up symmetric), act in fp32, act -> fp16, down in
-    fp32 (optionally rounded to fp16), weighted fp32 sum over the token's
-    routes in slot order.  Non-local ids (>= len(experts)) are skipped.
+    ``experts[e]`` holds dense matrices ``gate`` [H, I] (None for a gateless
+    layer), ``up`` [H, I], ``down`` [I, H] (fp16 as ``dequant`` produces them;
+    float32 matrices are used as given).  Rounding points, in order:
+
+    1. x is rounded to fp16 (the plugin casts activations to fp16 before
+       every EXL3 projection, exl3.py:2856 / 2396 ``.half()``);
+    2. g = x @ gate and u = x @ up in fp32; with ``gu_fp16`` (default) each
+       is rounded to fp16 -- the native kernel stores the GEMV tile results as
+       fp16 (csrc/p2b_moe.cu:284) and the reference's native contract test
+       rounds them (tests/test_native_moe_contract.py:104-105).  With
+       ``gu_fp16=False`` they stay fp32, as in the eager loop
+       (exl3.py:2392-2410, ``out_dtype=torch.float32``);
+    3. the activation (``moe_activation``) in fp32, rounded to fp16 before
+       the down projection (exl3.py:2410 ``.half()``);
+    4. d = act @ down in fp32, rounded to fp16 when ``round_down`` (the
+       contract test's ``.half()`` at tests/test_native_moe_contract.py:107);
+    5. out[t] += fp32(w[t,k]) * d, in slot order k = 0, 1, ... (the
+       deterministic combine order of csrc/p2b_moe.cu:1976-2008).
+
+    Ids are mapped by ``map_topk_to_local`` (with ``expert_map`` when given);
+    sentinel routes contribute nothing.
     """
     x = np.asarray(x)
     T, H = x.shape
-    ids = map_topk_to_local(ids, len(experts))
+    ids = map_topk_to_local(ids, len(experts), expert_map)
     out = np.zeros((T, H), dtype=np.float32)
-    xh = np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    xh = _f16(x)
     for t in range(T):
         for k in range(ids.shape[1]):
             e = int(ids[t, k])
@@ -237,24 +305,17 @@ def moe_reference(x: np.ndarray, ids: np.ndarray, weights: np.ndarray,
                 continue
             pack = experts[e]
             xv = xh[t:t + 1]
-            u = (xv @ pack["up"].astype(np.float32)).astype(np.float16).astype(np.float32)
-            if pack.get("gate") is None:
-                if limit is not None and limit > 0:
-                    u = np.clip(u, -limit, limit)
-                a = np.square(np.maximum(u, 0))
-            else:
-                g = (xv @ pack["gate"].astype(np.float32)).astype(np.float16).astype(np.float32)
-                if limit is not None and limit > 0:
-                    g = np.minimum(g, np.float32(limit))
-                    u = np.clip(u, -limit, limit)
-                if act == "swiglu_oai":
-                    a = (u + 1.0) * g * (1.0 / (1.0 + np.exp(-1.702 * g)))
-                else:
-                    a = silu(g) * u
-            a = a.astype(np.float32).astype(np.float16).astype(np.float32)
-            d = a @ pack["down"].astype(np.float32)
+            u = xv @ np.asarray(pack["up"], dtype=np.float32)
+            g = None
+            if pack.get("gate") is not None:
+                g = xv @ np.asarray(pack["gate"], dtype=np.float32)
+            if gu_fp16:
+                u = _f16(u)
+                g = None if g is None else _f16(g)
+            a = _f16(moe_activation(g, u, act, limit))
+            d = a @ np.asarray(pack["down"], dtype=np.float32)
             if round_down:
-                d = d.astype(np.float16).astype(np.float32)
+                d = _f16(d)
             out[t] += np.float32(weights[t, k]) * d[0]
     return out
 

@@ -49,10 +49,26 @@ def dense_gpu(experts: list, cb: int, device, only=None) -> dict:
     return out
 
 
-def torch_moe_reference(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, dense: dict,
+def dense_of_layer(layer: dict, ks: list, cb: int):
+    """dense(e) for a device layer built by synthetic.moe_layer_device: the
+    expert's three projections dequantised on the GPU (the HIP dequant is
+    pinned bit-exact to the oracle), one expert at a time to bound memory."""
+    store = layer["_store"]
+
+    def dense(e):
+        d = {}
+        for pi, p in enumerate(("gate", "up", "down")):
+            t, su, sv = store[9 * e + 3 * pi: 9 * e + 3 * pi + 3]
+            d[p] = C.dequant_trellis(t, su, sv, int(ks[e]), True, codebook=cb)
+        return d
+    return dense
+
+
+def torch_moe_reference(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, dense,
                         n_local: int, limit: float = 0.0, act: str = "silu") -> torch.Tensor:
     """Same semantics as oracle.moe_reference, vectorised per expert in torch
-    fp32 (dense[e] = {'gate','up','down'} fp16 device matrices)."""
+    fp32.  ``dense`` maps an expert id to {'gate','up','down'} fp16 matrices:
+    a dict, or a callable (experts are then materialised one at a time)."""
     T, H = x.shape
     xh = x.to(torch.float16).float()
     out = torch.zeros((T, H), dtype=torch.float32, device=x.device)
@@ -61,7 +77,7 @@ def torch_moe_reference(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tenso
     for e in torch.unique(ids[valid]).tolist():
         t_idx, k_idx = (ids == e).nonzero(as_tuple=True)
         h = xh.index_select(0, t_idx)
-        pk = dense[e]
+        pk = dense(e) if callable(dense) else dense[e]
         u = (h @ pk["up"].float()).half().float()
         if "gate" not in pk:
             if limit > 0:

@@ -261,3 +261,53 @@ def test_moe_from_checkpoint_packs(gpu):
     assert rel_l2(got, want) <= TOL
     got_p = C.moe_prefill(xd, idd, wd, et.tables, et.n_local, et.intermediate, **et.forward_kwargs())
     assert rel_l2(got_p, want) <= TOL
+
+
+def test_graph_replay_after_workspace_growth(gpu):
+    """A decode step captured at small T keeps replaying into live memory
+    after an eager call at a larger T grew the shared workspace: the superseded
+    workspace is kept, and replays stay bit-identical to eager launches."""
+    E, H, I, topk, T = 8, 256, 256, 4, 2
+    experts = _layer(58, E, H, I, 3, 0)
+    dl = S.to_device(experts, gpu)
+    dense = dense_gpu(experts, 0, gpu)
+    x = torch.from_numpy(S.activations(11, T, H)).to(gpu)
+    ids_np, w_np = S.softmax_topk(12, T, E, topk)
+    ids = torch.from_numpy(ids_np).to(gpu)
+    w = torch.from_numpy(w_np).to(gpu)
+    out = torch.empty((T, H), dtype=torch.float32, device=gpu)
+
+    def run():
+        _forward(dl, x, ids, w, E, I, 0, out=out)
+
+    run()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    # an eager call at a much larger T grows the workspace; then fill the
+    # freed-and-reused memory pool with NaN
+    Tb = 512
+    xb = torch.from_numpy(S.activations(13, Tb, H)).to(gpu)
+    ib, wb = S.softmax_topk(14, Tb, E, topk)
+    _forward(dl, xb, torch.from_numpy(ib).to(gpu), torch.from_numpy(wb).to(gpu), E, I, 0)
+    junk = [torch.full((1 << 20,), float("nan"), device=gpu) for _ in range(16)]
+    for rep in range(2):
+        x.copy_(torch.from_numpy(S.activations(300 + rep, T, H)))
+        ids_np, w_np = S.softmax_topk(400 + rep, T, E, topk)
+        ids.copy_(torch.from_numpy(ids_np))
+        w.copy_(torch.from_numpy(w_np))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        run()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, out), "replay after workspace growth must match eager"
+        assert rel_l2(out, torch_moe_reference(x, ids, w, dense, E)) <= TOL
+    for j in junk:
+        assert torch.isnan(j).all(), "a replay wrote into memory owned by other tensors"
+    del graph

@@ -728,7 +728,13 @@ __device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft
         fat_tile<CB, K, 8>(p, ft, lds);
 }
 
-template <int CB>
+// KSET 0: tiles of K 2..4 (every uniform-K launch and most of a mixed-K
+// one); tiles of any other per-expert K are left to the KSET 1 launch, which
+// a grouped launch with K tables adds: it computes K 5 and 6 and writes
+// zeros for any other K, as the reference's mixed-K tile switch does
+// (csrc/p2b_moe.cu:295-324).  Two kernels, so that the K 5/6 decode's
+// registers never weigh on the common kernel's allocation.
+template <int CB, int KSET>
 __global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fat_gemm_kernel(
     FatParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -736,11 +742,31 @@ __global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(2, 
     int K;
     FatParams pq = p;
     if (!fat_tile_of(p, pq, ft, K)) return;
-    switch (K) {
-        case 2: fat_tile_k<CB, 2>(pq, ft, lds); break;
-        case 3: fat_tile_k<CB, 3>(pq, ft, lds); break;
-        case 4: fat_tile_k<CB, 4>(pq, ft, lds); break;
-        default: break;  // rejected on the host
+    if constexpr (KSET == 0) {
+        switch (K) {
+            case 2: fat_tile_k<CB, 2>(pq, ft, lds); break;
+            case 3: fat_tile_k<CB, 3>(pq, ft, lds); break;
+            case 4: fat_tile_k<CB, 4>(pq, ft, lds); break;
+            default: break;  // the KSET 1 launch's tile
+        }
+    } else {
+        switch (K) {
+            case 2: case 3: case 4: break;  // the KSET 0 launch's tile
+            case 5: fat_tile_k<CB, 5>(pq, ft, lds); break;
+            case 6: fat_tile_k<CB, 6>(pq, ft, lds); break;
+            default: {
+                // unsupported K: the tile's outputs are zeros
+                const int ncols = min(kTN, p.N - ft.nt * kTN);
+                for (int i = threadIdx.x; i < ft.rows_valid * ncols; i += kFatThreads) {
+                    const int64_t o = (ft.out_row0 + i / ncols) * pq.ldo + (int64_t)ft.nt * kTN + i % ncols;
+                    if (pq.out_f32)
+                        reinterpret_cast<float*>(pq.out)[o] = 0.0f;
+                    else
+                        reinterpret_cast<uint16_t*>(pq.out)[o] = 0;
+                }
+                break;
+            }
+        }
     }
 }
 
@@ -752,8 +778,9 @@ inline size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 hipError_t init_fat_caps() {
     static const hipError_t st = [] {
         hipError_t e = hipSuccess;
-        const void* fns[] = {(const void*)fat_gemm_kernel<0>, (const void*)fat_gemm_kernel<1>,
-                             (const void*)fat_gemm_kernel<2>};
+        const void* fns[] = {(const void*)fat_gemm_kernel<0, 0>, (const void*)fat_gemm_kernel<1, 0>,
+                             (const void*)fat_gemm_kernel<2, 0>, (const void*)fat_gemm_kernel<0, 1>,
+                             (const void*)fat_gemm_kernel<1, 1>, (const void*)fat_gemm_kernel<2, 1>};
         for (const void* f : fns) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFatLds);
             if (r != hipSuccess) {
@@ -766,13 +793,27 @@ hipError_t init_fat_caps() {
     return st;
 }
 
-void launch_fat(int cb, const FatParams& p, hipStream_t st) {
+template <int KSET>
+void launch_fat_set(int cb, const FatParams& p, hipStream_t st) {
     const int grid = ((p.n_tiles + 7) / 8) * 8;
     switch (cb) {
-        case 0: fat_gemm_kernel<0><<<grid, kFatThreads, kFatLds, st>>>(p); break;
-        case 1: fat_gemm_kernel<1><<<grid, kFatThreads, kFatLds, st>>>(p); break;
-        default: fat_gemm_kernel<2><<<grid, kFatThreads, kFatLds, st>>>(p); break;
+        case 0: fat_gemm_kernel<0, KSET><<<grid, kFatThreads, kFatLds, st>>>(p); break;
+        case 1: fat_gemm_kernel<1, KSET><<<grid, kFatThreads, kFatLds, st>>>(p); break;
+        default: fat_gemm_kernel<2, KSET><<<grid, kFatThreads, kFatLds, st>>>(p); break;
     }
+}
+
+// The GEMM of one launch: the K 2..4 kernel, then, when the launch reads
+// per-expert K tables, the kernel for the other K values.
+hipError_t launch_fat(int cb, const FatParams& p, hipStream_t st) {
+    launch_fat_set<0>(cb, p, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (p.grouped && (p.ktab || (p.nproj > 1 && p.ktab2))) {
+        launch_fat_set<1>(cb, p, st);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 struct PrefillPlan {
@@ -856,8 +897,7 @@ static int fat_gemm_impl(const uint16_t* a, int64_t M, const int16_t* trellis, i
     p.n_tiles = (int)(mtiles * p.n_ntiles);
     profile_begin_call();
     profile_mark(0, st);
-    launch_fat(codebook, p, st);
-    EXL3_LAUNCHED();
+    EXL3_HIP(launch_fat(codebook, p, st));
     profile_mark(1, st);
     const int64_t units = M * (N / 128);
     fat_out_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(z, (int)M, (int)N, svh, scatter,
@@ -1000,8 +1040,7 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
     p.ktab2 = k_up;
     p.kuni2 = (int)K_up;
     p.out2 = y_u;
-    launch_fat(codebook, p, st);
-    EXL3_LAUNCHED();
+    EXL3_HIP(launch_fat(codebook, p, st));
     (void)gtab_su;
     profile_mark(3, st);
     {
@@ -1025,8 +1064,7 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
     p.n_ntiles = (int)((hidden + kTN - 1) / kTN);
     p.nproj = 1;
     p.n_tiles = pp.max_mtiles * p.n_ntiles;
-    launch_fat(codebook, p, st);
-    EXL3_LAUNCHED();
+    EXL3_HIP(launch_fat(codebook, p, st));
     profile_mark(5, st);
     {
         const int64_t units = T * ((hidden / 128 + kRowSpan - 1) / kRowSpan);

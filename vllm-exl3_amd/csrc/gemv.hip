@@ -447,7 +447,9 @@ __device__ __forceinline__ bool load_unit(const GemvParams& p, Cursor& c, int n_
             // wave-uniform, or every address derived from it (the stream's
             // buffer resource) would be treated as divergent
             c.K = __builtin_amdgcn_readfirstlane(kt ? (int)kt[e] : ku);
-            // a per-expert K outside {2, 3, 4} streams nothing (never misaddresses)
+            // a per-expert K outside {2, 3, 4} streams nothing here (never
+            // misaddresses): gemv_anyk_kernel computes that unit (K 5, 6) or
+            // writes its partials as zeros (any other K)
             return c.rows > 0 && c.K >= 2 && c.K <= 4;
         }
     }
@@ -894,6 +896,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         pr = MODE == kModeGateUp ? load_proj(p.gateless ? 1 : qsel) : load_proj(2);
     }
 
+    // a per-expert K outside {2, 3, 4} is gemv_anyk_kernel's unit: nothing
+    // is streamed or written here (workgroup-uniform, before any barrier)
+    if (pr.K < 2 || pr.K > 4) return;
     const int MRB = p.MRB;
     G.img = (MODE == kModeGateUp && qsel) ? p.x2 : p.x;
     G.tiles_n = p.out_features >> 4;
@@ -914,8 +919,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         switch (pr.K) {
             case 2: wg_projection<2, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
             case 3: wg_projection<3, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
-            case 4: wg_projection<4, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
-            default: break;  // rejected on the host
+            default: wg_projection<4, CB>(p, G, pr, stage, A, red, restage, wave, lane); break;
         }
         if ((MODE == kModeLinear || MODE == kModeBatched) && p.S == 1) {
             // single split: finish in place
@@ -935,6 +939,111 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         }
         __syncthreads();
       }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Mixed-K MoE units whose per-expert K (from the int8 K tables) is outside the
+// streaming kernels' {2, 3, 4}.  The reference's mixed-K tile switch computes
+// K 5 and 6 with a generic dequantising tile and zero-fills the tile for any
+// other value (csrc/p2b_moe.cu:295-324); this kernel does the same for the
+// units the streaming kernels skip, writing the same raw split partials, so
+// the consumer kernels need no change.  Workgroup = (slot, projection,
+// 128-column block); it exits at once for an expert of K 2..4 (the launch
+// costs a few microseconds when no such expert is routed) and otherwise
+// walks the splits and the slot's rows in groups of 16.  Per wave and tile
+// row: the 256*K bytes are staged in the wave's LDS slot, each lane decodes
+// its four tile indices per tile with a general window read (any K), and
+// one v_mfma_f32_16x16x32_f16 per tile accumulates, in the operand order of
+// the streaming kernels (same image rows, same permuted tile positions).
+// ---------------------------------------------------------------------------
+constexpr int kAnyKMaxBytes = 256 * 8;  // one tile row at K <= 8
+
+template <int CB, int MODE>
+__global__ __launch_bounds__(kThreads) void gemv_anyk_kernel(GemvParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage_all[kWaves][kAnyKMaxBytes];
+    __shared__ float red[kWaves][16][128];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nJB = p.out_features >> 7;
+    const int nq = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
+    const int item = blockIdx.x;
+    const int qsel = item % nq;
+    const int jb = (item / nq) % nJB;
+    const int slot = item / nq / nJB;
+    if (slot >= *p.n_active) return;
+    const int e = p.slot_expert[slot];
+    const bool up = MODE == kModeGateUp && (p.gateless || qsel);
+    const int8_t* ktab = MODE == kModeDown ? p.ktab[2] : up ? p.ktab[1] : p.ktab[0];
+    if (!ktab) return;
+    const int K = ktab[e];
+    if (K >= 2 && K <= 4) return;  // the streaming kernels' unit
+    const int64_t* ttab = MODE == kModeDown ? p.tab[6] : up ? p.tab[3] : p.tab[0];
+    const uint8_t* trellis = reinterpret_cast<const uint8_t*>(ttab[e]);
+    const uint16_t* img = reinterpret_cast<const uint16_t*>((MODE == kModeGateUp && qsel) ? p.x2 : p.x);
+    const int rows = p.slot_rows[slot], row_base = p.slot_start[slot];
+    const bool compute = K == 5 || K == 6;
+    const int tiles_n = p.out_features >> 4;
+    const int g = lane >> 4;
+    const int col_nu = sigma_col(lane & 15);
+    const int q4 = 4 * lane_q(lane);
+    uint8_t* st = stage_all[wave];
+    for (int s = 0; s < p.S; ++s) {
+        float* dst = p.ws + (((int64_t)qsel * p.S + s) * p.n_rows_ws + row_base) * p.out_features + jb * 128;
+        if (!compute) {
+            for (int i = tid; i < rows * 128; i += kThreads) dst[(int64_t)(i >> 7) * p.out_features + (i & 127)] = 0.0f;
+            continue;
+        }
+        const int kt0 = s * p.R_hb * 8, nkt = p.R_hb * 8;
+        const uint32_t nbits = 256u * K, n32 = 8u * K, tile_bytes = 32u * K;
+        for (int rg = 0; rg < rows; rg += 16) {
+            const int nr = min(16, rows - rg);
+            const int64_t arow = row_base + rg + min(lane & 15, nr - 1);
+            float4_t acc[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+            for (int kl = wave; kl < nkt; kl += kWaves) {
+                const int kt = kt0 + kl;
+                const uint8_t* src = trellis + ((size_t)kt * tiles_n + (size_t)jb * 8) * tile_bytes;
+                for (uint32_t off = lane * 16u; off < 8u * tile_bytes; off += 1024u)
+                    *reinterpret_cast<v4u*>(st + off) = *reinterpret_cast<const v4u*>(src + off);
+                __builtin_amdgcn_wave_barrier();
+                const uint32_t* ap = reinterpret_cast<const uint32_t*>(img + arow * p.x_stride + (int64_t)kt * 16 + 4 * g);
+                const half8_t a = dup4(ap[0], ap[1]);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const uint32_t* tw = reinterpret_cast<const uint32_t*>(st + t * tile_bytes);
+                    uint32_t b[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        // window of tile index q4 + i: stream bits
+                        // [(idx + 257) K - 16, (idx + 257) K) mod 256 K, MSB first
+                        const uint32_t bit = ((uint32_t)(q4 + i + 1) * K + nbits - 16u) % nbits;
+                        const uint32_t i0 = bit >> 5, i1 = i0 + 1 == n32 ? 0 : i0 + 1;
+                        const uint32_t win = funnel(tw[i0], tw[i1], 48u - (bit & 31u)) & 0xFFFFu;
+                        if constexpr (CB == kCbMul1)
+                            b[i] = (uint32_t)half_to_bits(decode_weight<kCbMul1>(win));
+                        else
+                            b[i] = cb_pair<CB>(win);
+                    }
+                    acc[t] = mfma16x16x32(a, b, acc[t]);
+                }
+                __builtin_amdgcn_wave_barrier();  // the stage is rewritten by the next tile row
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave][4 * g + i][t * 16 + col_nu] = acc[t][i];
+            __syncthreads();
+            for (int i = tid; i < nr * 128; i += kThreads) {
+                const int r = i >> 7, c = i & 127;
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) v += red[w][r][c];
+                dst[(int64_t)(rg + r) * p.out_features + c] = v;
+            }
+            __syncthreads();
+        }
     }
 }
 
@@ -1418,6 +1527,20 @@ hipError_t launch_gemv(int cb, int lk, const PhasePlan& ph, hipStream_t st, cons
     }
 }
 
+// The units of a mixed-K MoE phase whose K is outside {2, 3, 4}: one
+// workgroup per (slot, streamed projection, 128-column block).
+template <int MODE>
+hipError_t launch_anyk(int cb, int max_slots, int nq, hipStream_t st, const GemvParams& p) {
+    const int64_t grid = (int64_t)max_slots * nq * (p.out_features >> 7);
+    if (grid < 1 || grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+    switch (cb) {
+        case 0: gemv_anyk_kernel<0, MODE><<<(unsigned)grid, kThreads, 0, st>>>(p); break;
+        case 1: gemv_anyk_kernel<1, MODE><<<(unsigned)grid, kThreads, 0, st>>>(p); break;
+        default: gemv_anyk_kernel<2, MODE><<<(unsigned)grid, kThreads, 0, st>>>(p); break;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace exl3
 
@@ -1740,6 +1863,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     const int lk_gu = gateless ? (kt[1] ? 0 : (int)Ks[1])
                                : ((!kt[0] && !kt[1] && Ks[0] == Ks[1]) ? (int)Ks[0] : 0);
     EXL3_HIP(launch_gemv<kModeGateUp>(codebook, lk_gu, mp.gu, st, pg));
+    if ((!gateless && kt[0]) || kt[1]) EXL3_HIP(launch_anyk<kModeGateUp>(codebook, mp.max_slots, mp.nproj, st, pg));
 
     // down input rows: gate/up finished once per route
     GemvParams pd = p;
@@ -1763,6 +1887,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     // down: raw partials [S_d][routes][hidden]
     profile_mark(4, st);
     EXL3_HIP(launch_gemv<kModeDown>(codebook, kt[2] ? 0 : (int)Ks[2], mp.dn, st, pd));
+    if (kt[2]) EXL3_HIP(launch_anyk<kModeDown>(codebook, mp.max_slots, 1, st, pd));
 
     profile_mark(5, st);
     combine_kernel<<<(int)(T * (hidden / 128)), kCombineWaves * 64, 0, st>>>(
@@ -1772,3 +1897,4 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     profile_mark(6, st);
     return kOk;
 }
+

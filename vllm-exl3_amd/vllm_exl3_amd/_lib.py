@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
                              _i64, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _p, _p, _p],
     "exl3_profile_begin": [_i32],
     "exl3_profile_end": [_p, _i32, _p, _p],
+    "exl3_fill_hash_u32": [_p, _i64, ctypes.c_uint64, _p],
 }
 _RESTYPES = {"exl3_last_error": ctypes.c_char_p, "exl3_gemm_workspace_size": _i64,
              "exl3_moe_workspace_size": _i64, "exl3_fat_gemm_workspace_size": _i64,

@@ -104,30 +104,71 @@ def zipf_topk(seed: int, tokens: int, n_experts: int, topk: int, s: float = 1.1)
     return ids, w
 
 
+class DeviceBits:
+    """Seeded device-side bit streams from the library's counter-based fill
+    (``exl3_fill_hash_u32``): no library RNG kernel runs, and the bits are the
+    same on every device.  Each call draws a fresh stream (seed, counter)."""
+
+    def __init__(self, seed: int, device):
+        self.seed = int(seed) & 0xFFFFFFFF
+        self.device = device
+        self.n = 0
+
+    def words(self, n: int):
+        """n uint32 words as an int32 tensor."""
+        import torch
+
+        from . import _lib
+
+        t = torch.empty(n, dtype=torch.int32, device=self.device)
+        self.n += 1
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.call("exl3_fill_hash_u32", t.data_ptr(), n, (self.seed << 32) | self.n, stream)
+        return t
+
+    def uniform(self, n: int):
+        """n float32 values uniform on (0, 1): (24 high bits + 0.5) / 2^24."""
+        import torch
+
+        w = self.words(n)
+        return (torch.bitwise_right_shift(w, 8) & 0xFFFFFF).float().add_(0.5).mul_(2.0 ** -24)
+
+    def signs(self, n: int):
+        import torch
+
+        return torch.where((self.words(n) & 1) == 1, -1.0, 1.0)
+
+    def normal(self, shape):
+        """Standard normal float32 values by the Box-Muller transform."""
+        import math
+
+        import torch
+
+        n = int(np.prod(shape))
+        u1, u2 = self.uniform(n), self.uniform(n)
+        z = torch.sqrt(-2.0 * torch.log(u1)) * torch.cos((2.0 * math.pi) * u2)
+        return z.view(*shape)
+
+
 def moe_layer_device(seed: int, n_experts: int, hidden: int, inter: int, K, device) -> dict:
-    """Like ``to_device(moe_layer(...))`` but generated on the device with
-    torch's seeded generator (for multi-GB layers; the bits differ from the
-    numpy generator's, the distributions are the same).  ``K`` is an int or a
+    """Like ``to_device(moe_layer(...))`` but generated on the device from
+    ``DeviceBits`` (for multi-GB layers; the bits differ from the numpy
+    generator's, the distributions are the same).  ``K`` is an int or a
     per-expert sequence of ints."""
     import torch
 
-    gen = torch.Generator(device=device)
-    gen.manual_seed(seed)
+    gen = DeviceBits(seed, device)
 
     def bits(in_f, out_f, k):
-        t = torch.randint(-(1 << 15), 1 << 15, (in_f // 16, out_f // 16, 16 * k),
-                          dtype=torch.int32, device=device, generator=gen)
-        return t.to(torch.int16)
-
-    def signs(n):
-        return torch.where(torch.rand(n, device=device, generator=gen) < 0.5, -1.0, 1.0)
+        n = (in_f // 16) * (out_f // 16) * 16 * k
+        return gen.words(n // 2).view(torch.int16).view(in_f // 16, out_f // 16, 16 * k)
 
     def su(n):
-        return signs(n).half()
+        return gen.signs(n).half()
 
     def sv(n):
-        u = 0.005 + 0.015 * torch.rand(n, device=device, generator=gen)
-        return (signs(n) * u).half()
+        u = 0.005 + 0.015 * gen.uniform(n)
+        return (gen.signs(n) * u).half()
 
     store = []
     names = ("gate", "up", "down")
@@ -211,19 +252,21 @@ def block_table(seed: int, B: int, max_pages: int, num_pages: int | None = None)
 
 def kv_inputs_device(seed: int, B: int, Hkv: int, L: int, device, D: int = 128,
                      outlier_frac: float = 0.02, outlier_scale: float = 8.0):
-    """``kv_inputs`` generated on the device with torch's seeded generator
-    (for the full-size workload; bf16 tensors [B, Hkv, L, D])."""
+    """``kv_inputs`` generated on the device from ``DeviceBits`` (for the
+    full-size workload; bf16 tensors [B, Hkv, L, D]); the outlier channels
+    come from the numpy generator."""
     import torch
 
-    gen = torch.Generator(device=device)
-    gen.manual_seed(seed)
+    gen = DeviceBits(seed, device)
+    g = rng(seed)
     n_out = max(1, int(round(outlier_frac * D)))
     out = []
     for _ in range(2):
-        x = torch.randn((B, Hkv, L, D), device=device, generator=gen, dtype=torch.float32)
-        sc = torch.ones((Hkv, D), device=device)
+        x = gen.normal((B, Hkv, L, D))
+        sc = np.ones((Hkv, D), np.float32)
         for h in range(Hkv):
-            ch = torch.randperm(D, device=device, generator=gen)[:n_out]
-            sc[h, ch] = outlier_scale
-        out.append((x * sc[None, :, None, :]).to(torch.bfloat16))
+            sc[h, g.choice(D, size=n_out, replace=False)] = outlier_scale
+        x.mul_(torch.from_numpy(sc).to(device)[None, :, None, :])
+        out.append(x.to(torch.bfloat16))
+        del x
     return out[0], out[1]

@@ -105,6 +105,10 @@ def decode_tiles(trellis: torch.Tensor, K: int, mcg: bool, *, mul1: bool = False
 # next kernel in stream order)
 # ---------------------------------------------------------------------------
 _WORKSPACES: dict[tuple, torch.Tensor] = {}
+# Superseded workspaces are never freed: a HIP graph captured while one of
+# them was current keeps its address, and replays after a growth must not
+# write into memory the caching allocator has handed to other tensors.
+_RETIRED: list[torch.Tensor] = []
 
 _DTYPE_ID = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -115,18 +119,38 @@ def _dtype_id(t: torch.Tensor, what: str) -> int:
     return _DTYPE_ID[t.dtype]
 
 
+def _capturing(device: torch.device) -> bool:
+    return device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
+
 def workspace(device: torch.device, kind: str, nbytes: int) -> torch.Tensor:
-    """Per-(device, kind) scratch, grown on demand.
+    """Per-(device, kind) scratch, grown on demand and never freed.
 
     Like the reference's process-global temp caches (src/vllm_exl3/exl3.py:
     221-222, 2889) this is not thread-safe; calls sharing it must be ordered on
-    one stream.  Allocate outside graph capture (a first call sizes it)."""
+    one stream.  Growth keeps the old buffer alive (a captured graph may hold
+    its address) and grows by at least half, so the retired buffers total
+    less than twice the current one.  Growth is refused during graph capture:
+    call once eagerly at the largest size first, or ``reserve_workspace``."""
     key = (str(device), kind)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        if _capturing(device):
+            raise RuntimeError(
+                f"EXL3 workspace '{kind}' must grow to {int(nbytes)} bytes during graph capture; "
+                "run the call once eagerly at its largest size (or reserve_workspace) before capture")
+        size = max(int(nbytes), 256)
+        if ws is not None:
+            size = max(size, ws.numel() + ws.numel() // 2)
+            _RETIRED.append(ws)
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+def reserve_workspace(device: torch.device, kind: str, nbytes: int) -> torch.Tensor:
+    """Size a workspace ahead of graph capture (same rules as ``workspace``)."""
+    return workspace(torch.device(device), kind, nbytes)
 
 
 # ---------------------------------------------------------------------------
