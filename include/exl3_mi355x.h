@@ -123,6 +123,28 @@ int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hidden, int6
                      void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/* exl3_moe_forward without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The scratch is a
+ * 64 MiB device array inside the library (each GPU the library runs on holds
+ * it until the process ends); a call whose exl3_moe_workspace_size exceeds
+ * 64 MiB fails with EXL3_EINVAL before any launch.  Allocates nothing; runs
+ * on the device current on the calling thread.  All calls on one GPU share
+ * the array: calls ordered on one stream are fine, calls that overlap (other
+ * streams or threads) race.  Same arguments, validation and results as
+ * exl3_moe_forward. */
+int exl3_moe_forward_noalloc(const void* x, int x_dtype, int64_t T, int64_t hidden, int64_t inter,
+                             const int64_t* gate_trellis, const int64_t* gate_suh,
+                             const int64_t* gate_svh, const int64_t* up_trellis,
+                             const int64_t* up_suh, const int64_t* up_svh,
+                             const int64_t* down_trellis, const int64_t* down_suh,
+                             const int64_t* down_svh, int64_t n_local, const int8_t* k_gate,
+                             const int8_t* k_up, const int8_t* k_down, int64_t K_gate,
+                             int64_t K_up, int64_t K_down, int codebook, int gateless, int act,
+                             float swiglu_limit, const void* ids, int ids_dtype,
+                             const void* weights, int w_dtype, int64_t topk,
+                             const int32_t* n_valid, void* out, int out_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Prefill ("fat") GEMM: out[M, N] = had128(A x Wq) * svh in fp32, where A is
  * fp16 [M, K_in] row-major and already input-rotated by the caller (x * suh

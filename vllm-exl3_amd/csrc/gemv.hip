@@ -31,6 +31,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace exl3 {
 namespace {
@@ -1898,3 +1899,67 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     return kOk;
 }
 
+// ---------------------------------------------------------------------------
+// Decode MoE step without a caller workspace, for callers that cannot
+// allocate (code under HIP graph capture, tight serving loops, harnesses that
+// forbid hipMalloc).  The workspace of exl3_moe_forward comes from `scratch`,
+// a file-scope device array that every GPU the library runs on holds until
+// the process ends.  In host code the array's name is only a stand-in: its
+// device address, one per device, comes from hipGetSymbolAddress at the
+// first call on that device and is the only handle passed to kernels.  The
+// workspace needs no clearing (every element a kernel reads was written
+// earlier in the same call, in stream order), so calls that follow each other
+// on one stream may reuse it; calls that overlap on one GPU (other streams,
+// other threads) race on it.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on the current device.
+int scratch_ptr(void** out) {
+    int dev = -1;
+    EXL3_HIP(hipGetDevice(&dev));
+    EXL3_CHECK(dev >= 0 && dev < kMaxScratchDevices, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        EXL3_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        EXL3_CHECK(p != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return kOk;
+}
+}  // namespace
+
+EXL3_API int exl3_moe_forward_noalloc(const void* x, int x_dtype, int64_t T, int64_t hidden, int64_t inter,
+                                      const int64_t* gate_trellis, const int64_t* gate_suh,
+                                      const int64_t* gate_svh, const int64_t* up_trellis,
+                                      const int64_t* up_suh, const int64_t* up_svh,
+                                      const int64_t* down_trellis, const int64_t* down_suh,
+                                      const int64_t* down_svh, int64_t n_local, const int8_t* k_gate,
+                                      const int8_t* k_up, const int8_t* k_down, int64_t K_gate,
+                                      int64_t K_up, int64_t K_down, int codebook, int gateless, int act,
+                                      float swiglu_limit, const void* ids, int ids_dtype,
+                                      const void* weights, int w_dtype, int64_t topk,
+                                      const int32_t* n_valid, void* out, int out_dtype, void* stream) {
+    const int64_t need = exl3_moe_workspace_size(T, topk, n_local, hidden, inter, gateless);
+    EXL3_CHECK(need <= (int64_t)kNoAllocScratchBytes,
+               "fused MoE without a workspace: this call needs %lld bytes of scratch, the library's "
+               "scratch array holds %zu (call exl3_moe_forward with a workspace)",
+               (long long)need, kNoAllocScratchBytes);
+    void* ws = nullptr;
+    const int rc = scratch_ptr(&ws);
+    if (rc != kOk) return rc;
+    // exl3_moe_forward validates every argument (need == 0 for a rejected geometry)
+    return exl3_moe_forward(x, x_dtype, T, hidden, inter, gate_trellis, gate_suh, gate_svh, up_trellis,
+                            up_suh, up_svh, down_trellis, down_suh, down_svh, n_local, k_gate, k_up,
+                            k_down, K_gate, K_up, K_down, codebook, gateless, act, swiglu_limit, ids,
+                            ids_dtype, weights, w_dtype, topk, n_valid, out, out_dtype, ws,
+                            (int64_t)kNoAllocScratchBytes, stream);
+}

@@ -34,6 +34,9 @@ SIGNATURES: dict[str, list] = {
     "exl3_moe_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i32],
     "exl3_moe_forward": [_p, _i32, _i64, _i64, _i64] + [_p] * 9 + [_i64, _p, _p, _p, _i64, _i64, _i64,
                          _i32, _i32, _i32, _f32, _p, _i32, _p, _i32, _i64, _p, _p, _i32, _p, _i64, _p],
+    "exl3_moe_forward_noalloc": [_p, _i32, _i64, _i64, _i64] + [_p] * 9 + [_i64, _p, _p, _p, _i64, _i64,
+                                 _i64, _i32, _i32, _i32, _f32, _p, _i32, _p, _i32, _i64, _p, _p, _i32,
+                                 _p],
     "exl3_fat_gemm": [_p, _i64, _p, _i64, _i64, _i64, _i32, _p, _p, _p],
     "exl3_fat_gemm_workspace_size": [_i64, _i64, _i32],
     "exl3_fat_gemm_scatter": [_p, _i64, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _i64, _p, _i64,
