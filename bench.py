@@ -306,6 +306,49 @@ def kv_decode_c4(S, torch, dev, steps, warmup, PhaseTimer):
     }
 
 
+def crossover(args) -> int:
+    """Median µs per call of moe_forward (decode executor) and moe_prefill
+    (prefill executor) for T tokens, softmax top-8 routing, on two layer
+    geometries; one JSON line per (geometry, T)."""
+    import torch
+
+    from vllm_exl3_amd import synthetic as S
+    from vllm_exl3_amd import vllm_exl3_c as C
+
+    dev = torch.device("cuda", 0)
+    geoms = [("C1", 64, 2048, 1536, 3, 0), ("C2", 128, 4096, 1024, 4, 1)]
+    for name, E_, H_, I_, K_, cb in geoms:
+        layer = S.moe_layer_device(11, E_, H_, I_, K_, dev)
+        for T in (8, 16, 32, 48, 64, 96, 128, 192, 256, 384, 512, 1024):
+            x = torch.from_numpy(S.activations(T, T, H_)).to(dev).bfloat16()
+            ids_np, w_np = S.softmax_topk(T, T, E_, TOPK)
+            ids = torch.from_numpy(ids_np).to(dev)
+            w = torch.from_numpy(w_np).to(dev)
+            out = torch.empty((T, H_), dtype=torch.float32, device=dev)
+            res = {"geometry": name, "T": T}
+            for kind, fn in (("decode", C.moe_forward), ("prefill", C.moe_prefill)):
+                call = lambda: fn(x, ids, w, layer, E_, I_, K=(K_, K_, K_), codebook=cb, out=out)  # noqa: E731
+                res[kind + "_us"] = round(median_us(torch, call, 20, 3), 2)
+            print(json.dumps(res), flush=True)
+        del layer
+        torch.cuda.empty_cache()
+    return 0
+
+
+def median_us(torch, fn, n, warmup):
+    """Median of n single-call times (HIP events around each call)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in ev])) * 1e3
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -322,7 +365,12 @@ def main() -> int:
     ap.add_argument("--fat-probe", default="", metavar="M,K,N",
                     help="only run the fat GEMM (K4 MCG) on one dense M x K x N problem with "
                          "host-generated inputs, 5 launches, and exit (for rocprofv3 --pmc runs)")
+    ap.add_argument("--crossover", action="store_true",
+                    help="only time the decode and the prefill executor over a range of T on the "
+                         "C1 and C2 layer geometries (the dispatch threshold) and exit")
     args = ap.parse_args()
+    if args.crossover:
+        return crossover(args)
     if args.fat_probe:
         import numpy as np
         import torch

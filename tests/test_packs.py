@@ -84,7 +84,7 @@ def _sd():
     (lambda sd: sd.pop(f"{PREFIX}.1.w1.trellis"), "w1 for every expert"),
     (lambda sd: sd.__setitem__(f"{PREFIX}.0.w2.trellis", torch.zeros((8, 16, 48), dtype=torch.int16)),
      "does not match"),
-    (lambda sd: sd.__setitem__(f"{PREFIX}.0.w1.trellis", torch.zeros((8, 16, 80), dtype=torch.int16)),
+    (lambda sd: sd.__setitem__(f"{PREFIX}.0.w1.trellis", torch.zeros((8, 16, 112), dtype=torch.int16)),
      "supports K"),
     (lambda sd: sd.__setitem__(f"{PREFIX}.0.w1.trellis", torch.zeros((8, 16, 48), dtype=torch.int32)),
      "int16"),
@@ -116,3 +116,28 @@ def test_safetensors_file(tmp_path):
     save_file(sd, path)
     et = P.load_experts_safetensors(path, PREFIX, 3, "cpu")
     assert et.codebook == P.CB_MUL1 and et.k_tables[2].tolist() == [2, 3, 4]
+
+
+def test_k5_k6_packs_always_get_k_tables():
+    """K 5/6 run through the executors' per-expert K tables, so a layer with
+    such a K gets tables even when its K is uniform."""
+    sd = P.state_dict_of(S.moe_layer(10, 2, 128, 256, 5), PREFIX, P.CB_MCG)
+    et = P.load_experts(sd, PREFIX, 2, "cpu")
+    assert et.k_tables is not None and et.k_tables[0].tolist() == [5, 5]
+    sd = P.state_dict_of(S.moe_layer(11, 2, 128, 256, [(6, 5, 4), 3]), PREFIX, P.CB_MCG)
+    et = P.load_experts(sd, PREFIX, 2, "cpu")
+    assert [t.tolist() for t in et.k_tables] == [[6, 3], [5, 3], [4, 3]]
+    sd = P.state_dict_of(S.moe_layer(12, 2, 128, 256, 3), PREFIX, P.CB_MCG)
+    assert P.load_experts(sd, PREFIX, 2, "cpu").k_tables is None
+
+
+def test_attach_sets_dispatch_attributes():
+    from types import SimpleNamespace
+
+    sd = P.state_dict_of(S.moe_layer(13, 3, 128, 256, [2, 3, 4]), PREFIX, P.CB_MUL1)
+    et = P.load_experts(sd, PREFIX, 3, "cpu")
+    layer = et.attach(SimpleNamespace())
+    assert layer._exl3_ptrs is et.tables and layer._exl3_n_local == 3
+    assert layer._exl3_codebook == P.CB_MUL1 and layer._exl3_intermediate_local == 256
+    assert len(layer._exl3_inners) == 3 and layer._exl3_inners[2]["down"].K == 4
+    assert layer._exl3_inners[1]["up"].trellis.data_ptr() == int(et.tables["up_trellis"][1])

@@ -44,7 +44,9 @@ MUL1_MARKER_SIGNED_INT32 = -2082680531
 EXL3_SUFFIXES = ("trellis", "suh", "svh", "mcg", "mul1")
 PROJECTIONS = (("gate", "w1"), ("up", "w3"), ("down", "w2"))
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
-K_SUPPORTED = (2, 3, 4)
+# The executors stream K 2..4 and compute K 5/6 through per-expert K tables
+# (the reference's mixed-K range, csrc/p2b_moe.cu:295-324).
+K_SUPPORTED = (2, 3, 4, 5, 6)
 
 
 class PackError(RuntimeError):
@@ -68,6 +70,38 @@ class ExpertTables:
         """Keyword arguments of moe_forward / moe_prefill for these packs."""
         return {"K": self.K, "k_tables": self.k_tables, "codebook": self.codebook,
                 "gateless": self.gateless}
+
+    def inners(self) -> list[dict]:
+        """Per-expert projections as ``dispatch.Exl3Linear`` objects (the
+        reference's ``layer._exl3_inners``, used by the per-expert loop)."""
+        from .dispatch import Exl3Linear
+
+        out, i = [], 0
+        for e in range(self.n_local):
+            d = {"gate": None}
+            for p, _ in PROJECTIONS:
+                if p == "gate" and self.gateless:
+                    continue
+                t, su, sv = self._store[i:i + 3]
+                i += 3
+                d[p] = Exl3Linear(t, su, sv, self.ks[p][e], self.codebook)
+            out.append(d)
+        return out
+
+    def attach(self, layer):
+        """Set the layer attributes ``dispatch.apply_exl3_experts`` reads
+        (the names the reference's layer carries) and return the layer."""
+        layer._exl3_ptrs = self.tables
+        layer._exl3_k_tuple = self.K
+        layer._exl3_k_tables = self.k_tables
+        layer._exl3_codebook = self.codebook
+        layer._exl3_gateless = self.gateless
+        layer._exl3_intermediate_local = self.intermediate
+        layer._exl3_hidden_size = self.hidden
+        layer._exl3_n_local = self.n_local
+        layer._exl3_inners = self.inners()
+        layer._exl3_tables_owner = self
+        return layer
 
 
 def codebook_of(mcg: torch.Tensor | None, mul1: torch.Tensor | None, what: str,
@@ -186,7 +220,8 @@ def load_experts(get: Mapping[str, torch.Tensor] | Callable[[str], torch.Tensor 
             ptrs[f"gate_{a}"] = list(ptrs[f"up_{a}"])
         ks["gate"] = list(ks["up"])
     tables = {k: torch.tensor(v, dtype=torch.int64, device=device) for k, v in ptrs.items()}
-    uniform = all(len(set(ks[p])) == 1 for p, _ in PROJECTIONS)
+    # uniform tables only when every K is one the uniform-K launch streams
+    uniform = all(len(set(ks[p])) == 1 and ks[p][0] <= 4 for p, _ in PROJECTIONS)
     K = tuple(max(ks[p]) for p, _ in PROJECTIONS)
     k_tables = None if uniform else tuple(
         torch.tensor(ks[p], dtype=torch.int8, device=device) for p, _ in PROJECTIONS)
