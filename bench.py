@@ -5,7 +5,11 @@ Workload: one routed-MoE decode layer, 64 experts, top-8,
 hidden 2048, per-expert intermediate 1536, fused gate/up + SiLU + down, K3
 3INST trellis weights (seeded random bits, random suh/svh), bf16 activations
 N(0,1), softmax top-8 routing.  A step is one layer forward for a batch of T
-tokens; the headline is T = 16, with T = 1 and 4 reported alongside.
+tokens; the headline is T = 16, with T = 1 and 4 reported alongside.  Steps
+rotate over ``--layers`` distinct layers (default 5, 1.14 GB of packed
+experts), as consecutive layers of a model do, so the 256 MB Infinity Cache
+cannot serve a step's weights from the previous step: every step reads its
+experts from HBM.
 
 value = packed expert bytes touched per step (distinct routed experts x
 3,560,448 B + activations) / time per step, inputs resident in HBM.
@@ -13,12 +17,14 @@ roofline = the dominant kernel (the gate/up GEMV) timed live with HIP events
 on its launch stream, against the 8 TB/s HBM peak.
 cpu_baseline = the CPU oracle's eager per-expert loop (single-threaded dequant
 as the reference's host decoder, torch fp32 matmul on all host threads) on a
-time-bounded sample of the same routed experts.
+time-bounded sample of the same routed experts; the other configurations'
+CPU legs are reported under ``cpu_baselines``.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import pathlib
@@ -35,6 +41,8 @@ for p in (ROOT / "vllm-exl3_amd", ROOT / "oracle"):
 E, H, I, TOPK, K, CB = 64, 2048, 1536, 8, 3, 0
 EXPERT_BYTES = 3 * H * I * K // 8 + 2 * 3 * (H + I)  # trellis + suh/svh of 3 projections
 HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0  # MI355X published dense fp16/bf16 MFMA peak
+FP16_FLOP_PER_CLK_CU = 4096  # gfx950: 4 SIMDs x 1024 dense fp16 FLOP per clock
 # HBM bytes of one gate/up launch at T=16 (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000,
 # factors from a 256 MiB copy), from profiles/moe_decode_c1_t16.md; re-measured
 # with rocprofv3 --pmc whenever the kernel changes.
@@ -51,7 +59,64 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def run_batch(C, S, torch, layer, T, steps, warmup, dev, PhaseTimer):
+def gpu_peaks() -> dict:
+    """CU count and peak engine clock of device 0 (hipDeviceGetAttribute),
+    and the fp16 dense MFMA peak they give beside the published figure."""
+    out = {"published_tflops": FP16_PEAK_TFLOPS}
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+        cus, khz = ctypes.c_int(), ctypes.c_int()
+        # hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeClockRate (kHz)
+        if hip.hipDeviceGetAttribute(ctypes.byref(cus), 63, 0) == 0 and \
+                hip.hipDeviceGetAttribute(ctypes.byref(khz), 5, 0) == 0:
+            out.update({"cus": cus.value, "peak_clock_mhz": khz.value / 1e3,
+                        "fp16_flop_per_clk_cu": FP16_FLOP_PER_CLK_CU,
+                        "computed_tflops": round(cus.value * FP16_FLOP_PER_CLK_CU * khz.value * 1e3 / 1e12, 1)})
+    except OSError:
+        pass
+    return out
+
+
+def step_stats(ms: list) -> dict:
+    a = np.asarray(ms)
+    return {"mean_ms": float(a.mean()), "median_ms": float(np.median(a)),
+            "p95_ms": float(np.percentile(a, 95))}
+
+
+def graph_time_rot(torch, fns, steps, warmup) -> dict:
+    """Per-step times of fns[i % len(fns)] replayed from HIP graphs (one graph
+    per function, captured once): every kernel of a step runs on every replay,
+    only the host launch overhead is gone, as in a serving decode loop.  The K
+    timed steps are bracketed by events (mean) and each has its own pair
+    (median, p95)."""
+    graphs = []
+    for fn in fns:
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        graphs.append(g)
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        ev[i][0].record()
+        graphs[i % len(graphs)].replay()
+        ev[i][1].record()
+    end.record()
+    torch.cuda.synchronize()
+    st = step_stats([a.elapsed_time(b) for a, b in ev])
+    st["mean_ms"] = start.elapsed_time(end) / steps
+    del graphs
+    return st
+
+
+def run_batch(C, S, torch, layers, T, steps, warmup, dev, PhaseTimer):
     from vllm_exl3_amd.profiling import MOE_PHASES
 
     x = torch.from_numpy(S.activations(10 + T, T, H)).to(dev).bfloat16()
@@ -61,31 +126,43 @@ def run_batch(C, S, torch, layer, T, steps, warmup, dev, PhaseTimer):
     w = torch.from_numpy(w_np).to(dev)
     out = torch.empty((T, H), dtype=torch.float32, device=dev)
 
-    def step():
-        C.moe_forward(x, ids, w, layer, E, I, K=(K, K, K), codebook=CB, out=out)
+    def step_of(layer):
+        return lambda: C.moe_forward(x, ids, w, layer, E, I, K=(K, K, K), codebook=CB, out=out)
 
-    eager_ms, _ = time_steps(torch, step, steps, warmup)
-    ms = graph_time(torch, step, steps, warmup)
-    _, pt = time_steps(torch, step, steps, 1, PhaseTimer)
+    fns = [step_of(layer) for layer in layers]
+    cnt = [0]
+
+    def rotating():
+        fns[cnt[0] % len(fns)]()
+        cnt[0] += 1
+
+    ms, _ = time_steps(torch, rotating, steps, warmup)
+    st = event_stats(torch, rotating, steps, 1)
+    gr = graph_time_rot(torch, fns, steps, warmup)
+    _, pt = time_steps(torch, rotating, steps, 1, PhaseTimer)
     step_bytes = U * EXPERT_BYTES + 2 * T * H + 4 * T * H
     gu_bytes = U * 2 * (H * I * K // 8 + 2 * (H + I)) + 2 * T * H  # gate+up trellis, scales, x
     gu_ms = pt.mean_ms(MOE_PHASES.index("gate_up"))
     return {
         "T": T, "distinct_experts": U, "us_per_step": ms * 1e3, "gbs": step_bytes / (ms * 1e-3) / 1e9,
-        "eager_us_per_step": eager_ms * 1e3,
+        "median_us": st["median_ms"] * 1e3, "p95_us": st["p95_ms"] * 1e3,
+        "graph_us_per_step": gr["mean_ms"] * 1e3, "graph_median_us": gr["median_ms"] * 1e3,
         "phase_us": {n: pt.mean_ms(i) * 1e3 for i, n in enumerate(MOE_PHASES)},
         "gate_up_bytes": gu_bytes, "gate_up_gbs": gu_bytes / (gu_ms * 1e-3) / 1e9,
         "ids": ids_np, "x": x,
     }
 
 
-def cpu_baseline(S, O, torch, experts, ids_np, x, budget_s=12.0):
-    """The reference's CPU eager path on the routed experts of the batch, in
+def _dequant_f32(O, torch, q, K_, cb):
+    return torch.from_numpy(O.dequant(q["trellis"], q["suh"], q["svh"], K_, cb).astype(np.float32))
+
+
+def cpu_expert_loop(O, torch, experts, ks, cb, ids_np, x, budget_s, max_experts=None):
+    """The reference's CPU eager path over the routed experts of a batch, in
     routing order, until the time budget is spent: per expert, the host
     dequant (single-threaded, as csrc/bindings.cpp:15-100) of gate/up/down and
-    the fp32 matmuls of the per-expert loop (src/vllm_exl3/exl3.py:2357-2413)."""
-    import numpy as np
-
+    the fp32 matmuls of the per-expert loop (src/vllm_exl3/exl3.py:2357-2413).
+    Returns (experts done, experts routed, dequant s, matmul s, packed bytes)."""
     torch.set_num_threads(os.cpu_count() or 1)
     xf = x.float().cpu().to(torch.float16).float()
     order = []
@@ -95,10 +172,11 @@ def cpu_baseline(S, O, torch, experts, ids_np, x, budget_s=12.0):
     done, nbytes, t_dq, t_mm = 0, 0, 0.0, 0.0
     t0 = time.perf_counter()
     for e in order:
+        if max_experts is not None and done >= max_experts:
+            break
         pk = experts[e]
         t1 = time.perf_counter()
-        w = {p: torch.from_numpy(O.dequant(pk[p]["trellis"], pk[p]["suh"], pk[p]["svh"], K, CB)
-                                 .astype(np.float32)) for p in ("gate", "up", "down")}
+        w = {p: _dequant_f32(O, torch, pk[p], ks[e], cb) for p in ("gate", "up", "down")}
         t2 = time.perf_counter()
         rows = torch.from_numpy(np.nonzero((ids_np == e).any(axis=1))[0])
         h = xf.index_select(0, rows)
@@ -110,24 +188,131 @@ def cpu_baseline(S, O, torch, experts, ids_np, x, budget_s=12.0):
         t_dq += t2 - t1
         t_mm += t3 - t2
         done += 1
-        nbytes += EXPERT_BYTES
+        nbytes += sum(pk[p]["trellis"].nbytes + pk[p]["suh"].nbytes + pk[p]["svh"].nbytes
+                      for p in ("gate", "up", "down"))
         if time.perf_counter() - t0 > budget_s:
             break
+    return done, len(order), t_dq, t_mm, nbytes
+
+
+def cpu_baseline(S, O, torch, experts, ids_np, x, budget_s=12.0):
+    """C1 (the headline's CPU leg): the per-expert eager loop on a
+    time-bounded sample of the T=16 batch's routed experts."""
+    done, n, t_dq, t_mm, nbytes = cpu_expert_loop(O, torch, experts, [K] * E, CB, ids_np, x, budget_s)
     total = t_dq + t_mm
     return {
         "value": nbytes / total / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{done} of {len(order)} routed experts of the T={ids_np.shape[0]} batch "
+        "sample": (f"{done} of {n} routed experts of the T={ids_np.shape[0]} batch "
                    f"(dequant of gate/up/down single-threaded {t_dq:.2f} s + fp32 matmul "
                    f"{t_mm:.3f} s on {torch.get_num_threads()} threads; {cpu_model()}, "
                    f"os.cpu_count()={os.cpu_count()})"),
+        "dequant_s": round(t_dq, 3), "matmul_s": round(t_mm, 4),
     }
+
+
+def cpu_baselines(S, O, torch) -> dict:
+    """CPU legs of C0, C2, C3 and C4 on the host cores (the reference's CPU
+    eager path: single-threaded host dequant, torch fp32 matmul / attention on
+    all threads), each on a bounded sample; dequant and matmul timed apart.
+    Totals for a whole step are extrapolated from the sample and say so."""
+    torch.set_num_threads(os.cpu_count() or 1)
+    res = {"cores": torch.get_num_threads(), "cpu": cpu_model(), "os_cpu_count": os.cpu_count()}
+    # C0: one 2048x2048 K4 MCG linear, m = 1 and 16
+    lin = S.linear(0, 2048, 2048, 4)
+    t0 = time.perf_counter()
+    w = _dequant_f32(O, torch, lin, 4, 1)
+    t_dq = time.perf_counter() - t0
+    c0 = {"workload": "C0 2048x2048 K4 MCG", "dequant_s": round(t_dq, 4)}
+    for m in (1, 16):
+        xm = torch.from_numpy(S.activations(100 + m, m, 2048)).half().float()
+        t1 = time.perf_counter()
+        for _ in range(20):
+            _ = xm @ w
+        t_mm = (time.perf_counter() - t1) / 20
+        nbytes = 2048 * 2048 * 4 // 8 + 2 * 4096 + 2 * m * 4096
+        c0[f"m={m}"] = {"us": round((t_dq + t_mm) * 1e6, 1), "matmul_us": round(t_mm * 1e6, 1),
+                        "gbs": round(nbytes / (t_dq + t_mm) / 1e9, 4)}
+    res["c0"] = c0
+    # C2: routed prefill, E128 K4 MCG, T=2048 Zipf: a sample of experts
+    E2, H2, I2, T2 = 128, 4096, 1024, 2048
+    ids2, _ = S.zipf_topk(2, T2, E2, TOPK)
+    experts2 = S.moe_layer(2, 4, H2, I2, 4)  # the sample's packs (same shapes and K)
+    order = []
+    for e in ids2.ravel().tolist():
+        if e not in order:
+            order.append(e)
+    x2 = torch.from_numpy(S.activations(2, T2, H2))
+    t_dq = t_mm = 0.0
+    flops = 0.0
+    for i, e in enumerate(order[:4]):
+        pk = experts2[i]
+        t1 = time.perf_counter()
+        ws = {p: _dequant_f32(O, torch, pk[p], 4, 1) for p in ("gate", "up", "down")}
+        t2 = time.perf_counter()
+        rows = torch.from_numpy(np.nonzero((ids2 == e).any(axis=1))[0])
+        h = x2.index_select(0, rows).half().float()
+        g = (h @ ws["gate"]).half().float()
+        u = (h @ ws["up"]).half().float()
+        _ = ((torch.nn.functional.silu(g) * u).half().float()) @ ws["down"]
+        t_mm += time.perf_counter() - t2
+        t_dq += t2 - t1
+        flops += 2.0 * len(rows) * 3 * H2 * I2
+    rows_all = np.bincount(ids2.ravel(), minlength=E2)
+    per_dq = t_dq / 4
+    tot_flops = 2.0 * T2 * TOPK * 3 * H2 * I2
+    est_mm = t_mm / flops * tot_flops
+    res["c2"] = {"workload": "C2 E128 K4 MCG, T=2048 Zipf", "sample": "4 most-routed experts",
+                 "sample_rows": int(sum(rows_all[e] for e in order[:4])),
+                 "dequant_s_per_expert": round(per_dq, 3), "matmul_s_sample": round(t_mm, 3),
+                 "matmul_tflops": round(flops / t_mm / 1e12, 4),
+                 "step_s_extrapolated": round(per_dq * E2 + est_mm, 2),
+                 "tflops_extrapolated": round(tot_flops / (per_dq * E2 + est_mm) / 1e12, 5)}
+    # C3: mixed-K decode, a K2, a K3 and a K4 expert dequantised
+    H3, I3 = 6144, 2048
+    ks3 = S.mixed_k(3, 256) + [4]
+    per_k = {}
+    for kk in (2, 3, 4):
+        pk = S.moe_layer(30 + kk, 1, H3, I3, kk)[0]
+        t1 = time.perf_counter()
+        for p in ("gate", "up", "down"):
+            _dequant_f32(O, torch, pk[p], kk, 1)
+        per_k[kk] = time.perf_counter() - t1
+    ids3, _ = S.softmax_topk(3, 64, 256, TOPK)
+    used = sorted(set(ids3.ravel().tolist())) + [256]
+    est_dq = sum(per_k[ks3[e]] for e in used)
+    nbytes3 = sum(ks3[e] * 3 * H3 * I3 // 8 + 6 * (H3 + I3) for e in used)
+    res["c3"] = {"workload": "C3 E256+1 mixed K2/3/4 MCG, T=64",
+                 "dequant_s_per_expert": {f"K{kk}": round(v, 3) for kk, v in per_k.items()},
+                 "step_s_extrapolated": round(est_dq, 2),
+                 "gbs_extrapolated": round(nbytes3 / est_dq / 1e9, 4),
+                 "note": "matmul of 64 rows is negligible beside the dequant"}
+    # C4: int4 KV decode attention on the CPU, one KV head of one sequence
+    # (its 8 query heads): oracle dequant of the int4 cache + fp32 attention
+    L4, Hkv4, Hq4 = 32768, 8, 64
+    kf, vf = S.kv_inputs(4, 1, 1, L4)
+    kq, ksc, kz = O.kv_quantize_rows(kf)
+    vq, vsc, vz = O.kv_quantize_rows(vf)
+    q = torch.from_numpy(S.activations(4, Hq4 // Hkv4, 128))
+    t1 = time.perf_counter()
+    kd = torch.from_numpy(O.kv_dequantize_rows(kq, ksc, kz))[0]
+    vd = torch.from_numpy(O.kv_dequantize_rows(vq, vsc, vz))[0]
+    t2 = time.perf_counter()
+    att = torch.softmax((q[None] @ kd.transpose(1, 2)) / 128 ** 0.5, dim=-1)
+    _ = att @ vd
+    t3 = time.perf_counter()
+    n_units = 16 * Hkv4
+    res["c4"] = {"workload": "C4 B16 Hq64 Hkv8 d128 L32768 int4 KV",
+                 "sample": "1 KV head of 1 sequence (1 of 128 units)",
+                 "dequant_s_per_unit": round(t2 - t1, 3), "attention_s_per_unit": round(t3 - t2, 4),
+                 "step_s_extrapolated": round(n_units * (t3 - t1), 2),
+                 "gbs_extrapolated": round(L4 * 160 / (t3 - t1) / 1e9, 4)}
+    return res
 
 
 # ---------------------------------------------------------------------------
 # Other BASELINE configurations, reported beside the headline
 # ---------------------------------------------------------------------------
-FP16_PEAK_TFLOPS = 2500.0
 
 
 def time_steps(torch, fn, steps, warmup, PhaseTimer=None):
@@ -150,36 +335,36 @@ def time_steps(torch, fn, steps, warmup, PhaseTimer=None):
     return start.elapsed_time(end) / steps, pt
 
 
-def graph_time(torch, fn, steps, warmup):
-    """Milliseconds per call of fn replayed from a HIP graph: every kernel of
-    the step runs on every replay, only the host launch overhead is gone (a
-    serving decode loop replays captured steps the same way)."""
-    fn()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        fn()
+def event_stats(torch, fn, steps, warmup) -> dict:
+    """Eager per-call times: the K timed calls bracketed by events (mean)
+    and each with its own pair (median, p95)."""
     for _ in range(warmup):
-        g.replay()
+        fn()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(steps):
-        g.replay()
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    del g
-    return ms
+    st = step_stats([a.elapsed_time(b) for a, b in ev])
+    st["mean_ms"] = start.elapsed_time(end) / steps
+    return st
 
 
-def prefill_c2(C, S, torch, dev, steps, warmup, PhaseTimer):
+def prefill_c2(C, S, torch, dev, steps, warmup, PhaseTimer, zipf_s=1.1, peak_tflops=None):
     """Config 2: routed-MoE prefill, E128 top-8, H4096, I1024, K4 MCG,
-    T=2048 tokens with Zipf(1.1) expert popularity."""
+    T=2048 tokens with Zipf(s) expert popularity (s = 1.1 as BASELINE names
+    it; each token draws 8 distinct experts, so the head experts reach most
+    tokens: 16..1848 rows; s = 0.4 gives 70..510 rows, closer to the stated
+    ~0..~400 range).  The FLOP count is fixed by T x top-8 either way."""
     E2, H2, I2, T2, K2 = 128, 4096, 1024, 2048, 4
     layer2 = S.moe_layer_device(2, E2, H2, I2, K2, dev)
-    ids_np, w_np = S.zipf_topk(2, T2, E2, TOPK)
+    ids_np, w_np = S.zipf_topk(2, T2, E2, TOPK, s=zipf_s)
     x = torch.from_numpy(S.activations(2, T2, H2)).to(dev).bfloat16()
     ids = torch.from_numpy(ids_np).to(dev)
     w = torch.from_numpy(w_np).to(dev)
@@ -188,7 +373,9 @@ def prefill_c2(C, S, torch, dev, steps, warmup, PhaseTimer):
     def step():
         C.moe_prefill(x, ids, w, layer2, E2, I2, K=(K2, K2, K2), codebook=1, out=out)
 
-    ms, pt = time_steps(torch, step, steps, warmup, PhaseTimer)
+    st = event_stats(torch, step, steps, warmup)
+    ms = st["mean_ms"]
+    _, pt = time_steps(torch, step, steps, 1, PhaseTimer)
     routes = T2 * TOPK
     flops = 2.0 * routes * (2 * H2 * I2 + I2 * H2)
     gu_flops = 2.0 * routes * 2 * H2 * I2
@@ -197,17 +384,22 @@ def prefill_c2(C, S, torch, dev, steps, warmup, PhaseTimer):
     gemm_us = phase["gate_up_gemm"] + phase["down_gemm"]
     rows = np.bincount(ids_np.ravel(), minlength=E2)
     del layer2
-    return {
-        "workload": f"C2 routed-MoE prefill, E{E2} top-{TOPK}, H{H2} I{I2}, K{K2} MCG, T={T2}, Zipf(1.1)",
+    res = {
+        "workload": f"C2 routed-MoE prefill, E{E2} top-{TOPK}, H{H2} I{I2}, K{K2} MCG, T={T2}, Zipf({zipf_s})",
         "us_per_step": round(ms * 1e3, 2),
+        "median_us": round(st["median_ms"] * 1e3, 2), "p95_us": round(st["p95_ms"] * 1e3, 2),
         "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
         "frac_fp16_peak": round(flops / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
         "gemm_tflops": round(flops / (gemm_us * 1e-6) / 1e12, 2),
         "gate_up_gemm_tflops": round(gu_flops / (phase["gate_up_gemm"] * 1e-6) / 1e12, 2),
         "flops_per_step": flops,
-        "rows_per_expert": {"min": int(rows.min()), "max": int(rows.max())},
+        "rows_per_expert": {"min": int(rows.min()), "median": float(np.median(rows)),
+                            "max": int(rows.max())},
         "phase_us": {k: round(v, 2) for k, v in phase.items()},
     }
+    if peak_tflops:
+        res["frac_fp16_peak_computed"] = round(flops / (ms * 1e-3) / 1e12 / peak_tflops, 4)
+    return res
 
 
 def decode_c3(C, S, torch, dev, steps, warmup, PhaseTimer):
@@ -231,8 +423,9 @@ def decode_c3(C, S, torch, dev, steps, warmup, PhaseTimer):
         C.moe_forward(x, ids, w, layer3, E3 + 1, I3, K=(4, 4, 4), k_tables=layer3["k_tables"],
                       codebook=1, out=out)
 
-    eager_ms, _ = time_steps(torch, step, steps, warmup)
-    ms = graph_time(torch, step, steps, warmup)
+    ms, _ = time_steps(torch, step, steps, warmup)
+    st = event_stats(torch, step, steps, 1)
+    gr = graph_time_rot(torch, [step], steps, warmup)
     _, pt = time_steps(torch, step, steps, 1, PhaseTimer)
     used = sorted(set(ids_np.ravel().tolist()))
     nbytes = sum(ks[e] * 3 * H3 * I3 // 8 + 6 * (H3 + I3) for e in used) + 2 * T3 * H3 + 4 * T3 * H3
@@ -241,8 +434,9 @@ def decode_c3(C, S, torch, dev, steps, warmup, PhaseTimer):
         "workload": f"C3 mixed-K MoE decode, E{E3}+1 shared, top-{TOPK}, H{H3} I{I3}, "
                     f"K2/K3/K4 40/40/20 MCG, T={T3}",
         "us_per_step": round(ms * 1e3, 2),
-        "eager_us_per_step": round(eager_ms * 1e3, 2),
-        "timing": "HIP graph replay of the whole layer step; eager launches also reported",
+        "median_us": round(st["median_ms"] * 1e3, 2), "p95_us": round(st["p95_ms"] * 1e3, 2),
+        "graph_us_per_step": round(gr["mean_ms"] * 1e3, 2),
+        "timing": "eager launches of the whole layer step; HIP graph replay also reported",
         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_step": nbytes,
@@ -262,13 +456,16 @@ def linear_c0(C, S, torch, dev, steps, warmup):
     for m in (1, 16):
         x = torch.from_numpy(S.activations(100 + m, m, 2048)).to(dev).half()
         fn = lambda: C.exl3_gemm(x, t, su, sv, 4, True)  # noqa: E731
-        eager_ms, _ = time_steps(torch, fn, steps, warmup)
-        ms = graph_time(torch, fn, steps, warmup)
+        ms, _ = time_steps(torch, fn, steps, warmup)
+        st = event_stats(torch, fn, steps, 1)
+        gr = graph_time_rot(torch, [fn], steps, warmup)
         nbytes = 2048 * 2048 * 4 // 8 + 2 * 4096 + 2 * m * 4096
-        res[f"m={m}"] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                         "eager_us": round(eager_ms * 1e3, 2)}
+        res[f"m={m}"] = {"us": round(ms * 1e3, 2), "median_us": round(st["median_ms"] * 1e3, 2),
+                         "p95_us": round(st["p95_ms"] * 1e3, 2),
+                         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "graph_us": round(gr["mean_ms"] * 1e3, 2)}
     return {"workload": "C0 EXL3 linear 2048x2048, K4 MCG, fp16 x",
-            "timing": "HIP graph replay (rotate, GEMV, finish); eager launches also reported", **res}
+            "timing": "eager launches (rotate, GEMV, finish); HIP graph replay also reported", **res}
 
 
 def kv_decode_c4(S, torch, dev, steps, warmup, PhaseTimer):
@@ -287,8 +484,10 @@ def kv_decode_c4(S, torch, dev, steps, warmup, PhaseTimer):
     q = torch.from_numpy(S.activations(4, B4 * Hq4, 128).reshape(B4, Hq4, 128)).to(dev).bfloat16()
     out = torch.empty_like(q)
     scale = 1.0 / 128 ** 0.5
-    ms, pt = time_steps(torch, lambda: KV.int4_decode(q, pool, bt, st, Hkv4, scale, out),
-                        steps, warmup, PhaseTimer)
+    call = lambda: KV.int4_decode(q, pool, bt, st, Hkv4, scale, out)  # noqa: E731
+    ev = event_stats(torch, call, steps, warmup)
+    ms = ev["mean_ms"]
+    _, pt = time_steps(torch, call, steps, 1, PhaseTimer)
     cache_bytes = B4 * Hkv4 * L4 * 160
     nbytes = cache_bytes + 2 * q.numel() * 2 + bt.numel() * 4
     att_us = pt.mean_ms(0) * 1e3
@@ -297,6 +496,7 @@ def kv_decode_c4(S, torch, dev, steps, warmup, PhaseTimer):
         "workload": f"C4 int4 paged KV decode attention, B{B4} Hq{Hq4} Hkv{Hkv4} d128, "
                     f"L={L4}, 16-token pages",
         "us_per_step": round(ms * 1e3, 2),
+        "median_us": round(ev["median_ms"] * 1e3, 2), "p95_us": round(ev["p95_ms"] * 1e3, 2),
         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_step": nbytes,
@@ -335,6 +535,31 @@ def crossover(args) -> int:
     return 0
 
 
+def linear_crossover(args) -> int:
+    """Median µs of exl3_gemm on its GEMV path and on its fat path (forced by
+    EXL3_LINEAR_FAT_MIN_ROWS, which the library reads on every call) for m
+    rows, on C0's 2048x2048 K4 MCG weights and a 4096x4096 K3 layer."""
+    import torch
+
+    from vllm_exl3_amd import synthetic as S
+    from vllm_exl3_amd import vllm_exl3_c as C
+
+    dev = torch.device("cuda", 0)
+    for name, n, K_ in (("2048x2048 K4", 2048, 4), ("4096x4096 K3", 4096, 3)):
+        lin = S.linear(0, n, n, K_)
+        t, su, sv = (torch.from_numpy(lin[k]).to(dev) for k in ("trellis", "suh", "svh"))
+        for m in (16, 32, 64, 96, 128, 192, 256, 512, 1024, 2048):
+            x = torch.from_numpy(S.activations(m, m, n)).to(dev).half()
+            res = {"linear": name, "m": m}
+            for kind, rows in (("gemv", str(1 << 30)), ("fat", "1")):
+                os.environ["EXL3_LINEAR_FAT_MIN_ROWS"] = rows
+                res[kind + "_us"] = round(median_us(torch, lambda: C.exl3_gemm(x, t, su, sv, K_, True),
+                                                    20, 3), 2)
+            os.environ.pop("EXL3_LINEAR_FAT_MIN_ROWS", None)
+            print(json.dumps(res), flush=True)
+    return 0
+
+
 def median_us(torch, fn, n, warmup):
     """Median of n single-call times (HIP events around each call)."""
     for _ in range(warmup):
@@ -357,6 +582,8 @@ def main() -> int:
     ap.add_argument("--batches", default="1,4,16",
                     help="decode batch sizes T to run; the headline is the largest")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layers", type=int, default=5,
+                    help="distinct C1 layers the decode steps rotate over (HBM-resident weights)")
     ap.add_argument("--configs", default="c0,c2,c3,c4",
                     help="other BASELINE configs reported beside the headline (c0,c2,c3,c4; '' = none)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -368,9 +595,13 @@ def main() -> int:
     ap.add_argument("--crossover", action="store_true",
                     help="only time the decode and the prefill executor over a range of T on the "
                          "C1 and C2 layer geometries (the dispatch threshold) and exit")
+    ap.add_argument("--linear-crossover", action="store_true",
+                    help="only time the dense linear's GEMV and fat paths over a range of m and exit")
     args = ap.parse_args()
     if args.crossover:
         return crossover(args)
+    if args.linear_crossover:
+        return linear_crossover(args)
     if args.fat_probe:
         import numpy as np
         import torch
@@ -421,10 +652,12 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     experts = S.moe_layer(1, E, H, I, K)
-    layer = S.to_device(experts, dev)
+    layers = [S.to_device(experts, dev)] + [S.moe_layer_device(100 + i, E, H, I, K, dev)
+                                            for i in range(1, max(1, args.layers))]
     batches = sorted({int(b) for b in args.batches.split(",")})
-    results = {T: run_batch(C, S, torch, layer, T, args.steps, args.warmup, dev, PhaseTimer)
+    results = {T: run_batch(C, S, torch, layers, T, args.steps, args.warmup, dev, PhaseTimer)
                for T in batches}
+    peaks = gpu_peaks()
     T_head = batches[-1]
     head = results[T_head]
     line = {
@@ -440,13 +673,20 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic",
-        "timing": "HIP graph replay of the whole layer step (route, rotate, gate/up, act, down, "
-                  "combine); per-phase kernel times from a separate eager pass",
+        "timing": "eager launches of the whole layer step on one stream (K steps bracketed by HIP "
+                  f"events), steps rotating over {len(layers)} distinct layers "
+                  f"({len(layers) * E * EXPERT_BYTES / 1e9:.2f} GB of packed experts, beyond the "
+                  "256 MB Infinity Cache); median/p95 from a second pass with an event pair per "
+                  "step; HIP-graph replay reported beside it; per-phase kernel times from a third "
+                  "eager pass",
+        "median_ms_per_step": round(head["median_us"] / 1e3, 6),
+        "p95_ms_per_step": round(head["p95_us"] / 1e3, 6),
         "config": {
             "workload": f"C1 routed-MoE decode layer, E64 top-8, H2048 I1536, K3 3INST, bf16 x, T={T_head}",
             "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "K": K, "codebook": "3INST",
-            "tokens": T_head, "distinct_experts": head["distinct_experts"],
+            "tokens": T_head, "distinct_experts": head["distinct_experts"], "layers": len(layers),
         },
+        "peaks": {"hbm_gbs": HBM_PEAK_GBS, "fp16": peaks},
         "roofline": {
             "bound": "hbm",
             "kernel": "gemv_wg_kernel<3INST, gate/up>",
@@ -461,7 +701,9 @@ def main() -> int:
         },
         "per_batch": {
             f"T={T}": {"us_per_step": round(r["us_per_step"], 2), "GB/s": round(r["gbs"], 1),
-                       "eager_us_per_step": round(r["eager_us_per_step"], 2),
+                       "median_us": round(r["median_us"], 2), "p95_us": round(r["p95_us"], 2),
+                       "graph_us_per_step": round(r["graph_us_per_step"], 2),
+                       "graph_median_us": round(r["graph_median_us"], 2),
                        "distinct_experts": r["distinct_experts"],
                        "phase_us": {k: round(v, 2) for k, v in r["phase_us"].items()}}
             for T, r in results.items()
@@ -471,8 +713,11 @@ def main() -> int:
     if "c0" in others:
         line["linear_c0"] = linear_c0(C, S, torch, dev, args.steps, args.warmup)
     if "c2" in others:
+        pk = peaks.get("computed_tflops")
         line["prefill_c2"] = prefill_c2(C, S, torch, dev, max(5, args.steps // 5),
-                                        min(args.warmup, 3), PhaseTimer)
+                                        min(args.warmup, 3), PhaseTimer, peak_tflops=pk)
+        line["prefill_c2_flat"] = prefill_c2(C, S, torch, dev, max(5, args.steps // 5),
+                                             min(args.warmup, 3), PhaseTimer, zipf_s=0.4, peak_tflops=pk)
     if "c3" in others:
         line["mixed_k_c3"] = decode_c3(C, S, torch, dev, args.steps, args.warmup, PhaseTimer)
     if "c4" in others:
@@ -481,6 +726,8 @@ def main() -> int:
         import oracle as O
 
         line["cpu_baseline"] = cpu_baseline(S, O, torch, experts, head["ids"], head["x"])
+        if others:
+            line["cpu_baselines"] = cpu_baselines(S, O, torch)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -60,18 +60,28 @@ int exl3_decode_tiles(const int16_t* trellis, int64_t tiles_k, int64_t tiles_n, 
 
 
 /* ---------------------------------------------------------------------------
- * Decode GEMV / GEMM (streams packed trellis, fused input and output
- * rotations).  x is [m, in] (x_dtype 0 fp16, 1 bf16, 2 fp32; values are
- * rounded to fp16 first, as the reference casts at its boundary), out is
- * [m, out] of out_dtype.  K in {2,3,4}; any m >= 1 (rows are processed in
- * groups of 16 with the weights streamed once per group).
+ * Dense EXL3 linear (fused input and output rotations).  x is [m, in]
+ * (x_dtype 0 fp16, 1 bf16, 2 fp32; values are rounded to fp16 first, as the
+ * reference casts at its boundary), out is [m, out] of out_dtype.  K in
+ * {2,3,4}; 1 <= m <= 2^26.  Below 128 rows the decode GEMV streams the packed
+ * trellis once per group of 16 rows; from 128 rows the input rows are
+ * rotated once, one fat GEMM decodes the weights once per 256 rows on MFMA
+ * (fp32 accumulation) and an output pass applies the rotation x svh.
+ * exl3_linear adds an optional bias [out] (bias_dtype as x_dtype; NULL = no
+ * bias) after the rotation, where the reference adds it after its forward
+ * (Exl3LinearMethod.apply, src/vllm_exl3/exl3.py:6641-6654).
  * Replaces vllm_exl3_c.exl3_gemv (csrc/bindings.cpp:134-147,
- * csrc/exl3_gemv.cu:23-63) and vllm_exl3_c.exl3_gemm (csrc/bindings.cpp:110-115,
- * csrc/exl3_gemm.cu:8-31). */
+ * csrc/exl3_gemv.cu:23-63), vllm_exl3_c.exl3_gemm (csrc/bindings.cpp:110-115,
+ * csrc/exl3_gemm.cu:8-31) and the reconstruct + hgemm route of the dense
+ * forward above 144 rows (_dense_forward, src/vllm_exl3/exl3.py:5797-5819). */
 int64_t exl3_gemm_workspace_size(int64_t m, int64_t in_features, int64_t out_features);
 int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* trellis, int64_t tiles_k,
               int64_t tiles_n, int64_t K, int codebook, const uint16_t* suh, const uint16_t* svh,
               void* out, int out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+int exl3_linear(const void* x, int x_dtype, int64_t m, const int16_t* trellis, int64_t tiles_k,
+                int64_t tiles_n, int64_t K, int codebook, const uint16_t* suh, const uint16_t* svh,
+                const void* bias, int bias_dtype, void* out, int out_dtype, void* workspace,
+                int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Batched decode GEMV: one linear per listed expert over the same input rows,

@@ -32,6 +32,7 @@
 // and svh where it is otherwise memory-bound.
 #include "exl3_common.h"
 #include "gemv_core.h"
+#include "linear.h"
 #include "profile.h"
 #include "route.h"
 
@@ -540,6 +541,66 @@ __global__ __launch_bounds__(256) void fat_out_kernel(const float* src, int M, i
     }
 }
 
+// Dense linear, large m: A[row] = fp16(had128(fp16(x[row]) * suh) / sqrt(128)).
+// One wave per (row, kRowSpan 128-column blocks).
+__global__ __launch_bounds__(256) void linear_rotate_kernel(const void* x, int x_dtype, int H,
+                                                            const uint16_t* suh, uint16_t* a,
+                                                            int64_t n_units) {
+    const int lane = threadIdx.x & 63;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= n_units) return;
+    const int nb = H >> 7, ng = (nb + kRowSpan - 1) / kRowSpan;
+    const int64_t row = unit / ng;
+    const int j0 = (int)(unit % ng) * kRowSpan;
+    const RowCols rc = row_cols(j0, nb, lane);
+    float xv[kRowGroups][8], sv[kRowGroups][8];
+#pragma unroll
+    for (int g = 0; g < kRowGroups; ++g) {
+        ld_act8(x, x_dtype, row * H + rc.col[g], xv[g]);
+        ld_f16x8(suh, rc.col[g], sv[g]);
+    }
+#pragma unroll
+    for (int g = 0; g < kRowGroups; ++g) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[g][i] *= sv[g][i];
+        had128_x8(xv[g], lane);
+        if (rc.ok[g]) st_f16x8(a, row * H + rc.col[g], xv[g], kHadNorm);
+    }
+}
+
+// Dense linear, large m: out[row] = had128(Z[row]) * svh (+ bias), Z = A Wq /
+// sqrt(128) in fp32 from the GEMM.  One wave per (row, kRowSpan blocks).
+__global__ __launch_bounds__(256) void linear_out_kernel(const float* z, int N, const uint16_t* svh,
+                                                         const void* bias, int bias_dtype, void* out,
+                                                         int out_dtype, int64_t n_units) {
+    const int lane = threadIdx.x & 63;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= n_units) return;
+    const int nb = N >> 7, ng = (nb + kRowSpan - 1) / kRowSpan;
+    const int64_t row = unit / ng;
+    const int j0 = (int)(unit % ng) * kRowSpan;
+    const RowCols rc = row_cols(j0, nb, lane);
+    float v[kRowGroups][8], h[kRowGroups][8];
+#pragma unroll
+    for (int g = 0; g < kRowGroups; ++g) {
+        const float4_t* p = reinterpret_cast<const float4_t*>(z + row * N + rc.col[g]);
+        const float4_t a = p[0], b = p[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[g][k] = a[k];
+            v[g][4 + k] = b[k];
+        }
+        ld_f16x8(svh, rc.col[g], h[g]);
+    }
+#pragma unroll
+    for (int g = 0; g < kRowGroups; ++g) {
+        had128_x8(v[g], lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[g][i] = v[g][i] * h[g][i] + load_bias(bias, bias_dtype, rc.col[g] + i);
+        if (rc.ok[g]) st_out8(out, out_dtype, row * N + rc.col[g], v[g]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // The GEMM tile: 256 x 256 outputs computed by 8 waves (2 row halves x 4
 // column quarters, 128 x 64 each, 128 accumulator registers), two waves per
@@ -840,6 +901,55 @@ PrefillPlan plan_prefill(int64_t T, int64_t topk, int64_t n_local, int64_t H, in
 }
 
 }  // namespace
+
+size_t linear_fat_workspace_bytes(int64_t m, int64_t in_f, int64_t out_f) {
+    return a256(2 * (size_t)m * in_f) + a256(4 * (size_t)m * out_f);
+}
+
+int linear_fat(const void* x, int x_dtype, int64_t m, const int16_t* trellis, int64_t tiles_k,
+               int64_t tiles_n, int64_t K, int codebook, const uint16_t* suh, const uint16_t* svh,
+               const void* bias, int bias_dtype, void* out, int out_dtype, void* workspace,
+               hipStream_t st) {
+    EXL3_HIP(init_fat_caps());
+    const int64_t in_f = tiles_k * 16, out_f = tiles_n * 16;
+    uint16_t* a = reinterpret_cast<uint16_t*>(workspace);
+    float* z = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + a256(2 * (size_t)m * in_f));
+    profile_begin_call();
+    profile_mark(0, st);
+    {
+        const int64_t units = m * ((in_f / 128 + kRowSpan - 1) / kRowSpan);
+        linear_rotate_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(x, x_dtype, (int)in_f, suh, a,
+                                                                          units);
+        EXL3_LAUNCHED();
+    }
+    profile_mark(1, st);
+    FatParams p = {};
+    p.a = a;
+    p.lda = in_f;
+    p.trellis = reinterpret_cast<const uint8_t*>(trellis);
+    p.kuni = (int)K;
+    p.K_in = (int)in_f;
+    p.N = (int)out_f;
+    p.out = z;
+    p.out_f32 = 1;
+    p.ldo = out_f;
+    p.out_scale = kHadNorm;
+    p.grouped = 0;
+    p.M = (int)m;
+    p.n_ntiles = (int)((out_f + kTN - 1) / kTN);
+    p.n_tiles = (int)(((m + kTM - 1) / kTM) * p.n_ntiles);
+    EXL3_HIP(launch_fat(codebook, p, st));
+    profile_mark(2, st);
+    {
+        const int64_t units = m * ((out_f / 128 + kRowSpan - 1) / kRowSpan);
+        linear_out_kernel<<<(unsigned)((units + 3) / 4), 256, 0, st>>>(z, (int)out_f, svh, bias, bias_dtype,
+                                                                       out, out_dtype, units);
+        EXL3_LAUNCHED();
+    }
+    profile_mark(3, st);
+    return kOk;
+}
+
 }  // namespace exl3
 
 using namespace exl3;

@@ -25,6 +25,7 @@
 // balanced range of units per workgroup with its trellis pipeline kept full
 // across them.
 #include "gemv_core.h"
+#include "linear.h"
 #include "profile.h"
 #include "route.h"
 
@@ -647,6 +648,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
                 for (int r = wave; r < nr; r += kWaves) {
                     float v0 = red_sum(red, MRB, r, lane), v1 = red_sum(red, MRB, r, lane + 64);
                     finish_block(v0, v1, svh, cur.j * 128 + lane, lane);
+                    v0 += load_bias(p.bias, p.bias_dtype, cur.j * 128 + lane);
+                    v1 += load_bias(p.bias, p.bias_dtype, cur.j * 128 + lane + 64);
                     const int64_t o = (int64_t)(cur.row_base + cur.rg + r) * p.out_stride + cur.j * 128 + lane;
                     store_out(p.out, p.out_dtype, o, v0);
                     store_out(p.out, p.out_dtype, o + 64, v1);
@@ -927,6 +930,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
             for (int r = wave; r < G.nr; r += kWaves) {
                 float v0 = red_sum(red, MRB, r, lane), v1 = red_sum(red, MRB, r, lane + 64);
                 finish_block(v0, v1, pr.svh, G.j * 128 + lane, lane);
+                v0 += load_bias(p.bias, p.bias_dtype, G.j * 128 + lane);
+                v1 += load_bias(p.bias, p.bias_dtype, G.j * 128 + lane + 64);
                 const int64_t o = (int64_t)(G.row_base + G.rg + r) * p.out_stride + G.j * 128 + lane;
                 store_out(p.out, p.out_dtype, o, v0);
                 store_out(p.out, p.out_dtype, o + 64, v1);
@@ -1055,6 +1060,8 @@ struct FinishBatch {
     const int64_t* svh_tab;  // null: single linear
     const int* expert_list;
     int batch_m, n_ptr;
+    const void* bias;        // single linear: optional bias [out_f]
+    int bias_dtype;
 };
 
 __global__ __launch_bounds__(256) void linear_finish_kernel(const float* __restrict__ ws, int S,
@@ -1076,6 +1083,8 @@ __global__ __launch_bounds__(256) void linear_finish_kernel(const float* __restr
     if (!zero) {
         sum_splits(ws + (int64_t)r * out_f, (int64_t)m * out_f, S, j * 128 + lane, v0, v1);
         finish_block(v0, v1, svh, j * 128 + lane, lane);
+        v0 += load_bias(fb.bias, fb.bias_dtype, j * 128 + lane);
+        v1 += load_bias(fb.bias, fb.bias_dtype, j * 128 + lane + 64);
     }
     const int64_t o = (int64_t)r * out_f + j * 128 + lane;
     store_out(out, out_dtype, o, v0);
@@ -1330,13 +1339,22 @@ inline int pick_chunk_wg(int R_hb, int MRB) {
     return c < R_hb ? c : R_hb;
 }
 
+// EXL3_GEMV_SPLITS=S restricts the planners to that split count when it is
+// valid for the phase (tuning; read on every plan, workspace queries included).
+inline int gemv_forced_splits() {
+    const char* v = std::getenv("EXL3_GEMV_SPLITS");
+    return v ? std::atoi(v) : 0;
+}
+
 inline PhasePlan plan_phase_wg(int in_f, int out_f, int wg_items, int MRB) {
     const int n_hb = in_f / 128, n_j = out_f / 128;
     const int cap = resident_workgroups();
     PhasePlan best = {1, n_hb, pick_chunk_wg(n_hb, MRB), 1, 1, 0};
     double best_t = 1e30;
+    const int forced = gemv_forced_splits();
     for (int S = 1; S <= kMaxSplits && S <= n_hb; ++S) {
         if (n_hb % S) continue;
+        if (forced > 0 && S != forced && n_hb % forced == 0) continue;
         const int R_hb = n_hb / S;
         const int64_t items = (int64_t)wg_items * n_j * S;
         const int64_t rounds = (items + cap - 1) / cap;
@@ -1384,10 +1402,13 @@ inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, i
     PhasePlan best = {1, n_hb, pick_chunk(n_hb, MRB), 1, 0, 0};
     double best_t = 1e30;
     int64_t best_per_wg = 0;
+    const int forced = gemv_forced_splits();
     for (int S = 1; S <= kMaxSplits && S <= n_hb; ++S) {
         if (n_hb % S) continue;
         const int R_hb = n_hb / S;
         if (n_hb % 4 == 0 && R_hb % 4 != 0) continue;
+        if (forced > 0 && S != forced && n_hb % forced == 0 && (n_hb % 4 != 0 || (n_hb / forced) % 4 == 0))
+            continue;
         const int C_hb = pick_chunk(R_hb, MRB);
         const int nc = (R_hb + C_hb - 1) / C_hb;
         const int64_t units = (int64_t)est_items * n_j * S;
@@ -1550,29 +1571,49 @@ using namespace exl3;
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
+// Rows from which the dense linear takes the fat path; EXL3_LINEAR_FAT_MIN_ROWS
+// overrides the measured default (for testing and tuning; read on every call,
+// by the workspace query and the launch alike).
+static int64_t linear_fat_min_rows() {
+    const char* v = std::getenv("EXL3_LINEAR_FAT_MIN_ROWS");
+    if (v && *v) {
+        const long long r = std::atoll(v);
+        if (r >= 1) return r;
+    }
+    return kLinearFatMinRows;
+}
+
 EXL3_API int64_t exl3_gemm_workspace_size(int64_t m, int64_t in_features, int64_t out_features) {
     if (m < 1 || in_features < 128 || out_features < 128) return 0;
+    if (m >= linear_fat_min_rows()) return (int64_t)linear_fat_workspace_bytes(m, in_features, out_features);
     return (int64_t)plan_linear(m, in_features, out_features).total;
 }
 
-EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* trellis,
-                       int64_t tiles_k, int64_t tiles_n, int64_t K, int codebook,
-                       const uint16_t* suh, const uint16_t* svh, void* out, int out_dtype,
-                       void* workspace, int64_t workspace_bytes, void* stream) {
+EXL3_API int exl3_linear(const void* x, int x_dtype, int64_t m, const int16_t* trellis,
+                         int64_t tiles_k, int64_t tiles_n, int64_t K, int codebook,
+                         const uint16_t* suh, const uint16_t* svh, const void* bias, int bias_dtype,
+                         void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
     EXL3_CHECK(K == 2 || K == 3 || K == 4, "exl3_gemm supports K in {2, 3, 4}");
     EXL3_CHECK(codebook >= 0 && codebook <= 2, "codebook must be 0 (3INST), 1 (MCG) or 2 (mul1)");
-    EXL3_CHECK(x_dtype >= 0 && x_dtype <= 2 && out_dtype >= 0 && out_dtype <= 2,
+    EXL3_CHECK(x_dtype >= 0 && x_dtype <= 2 && out_dtype >= 0 && out_dtype <= 2 &&
+                   (!bias || (bias_dtype >= 0 && bias_dtype <= 2)),
                "dtype ids: 0 fp16, 1 bf16, 2 fp32");
-    EXL3_CHECK(m >= 1 && m <= 0x7FFFFFFF, "exl3_gemm needs 1 <= m < 2^31");
+    EXL3_CHECK(m >= 1 && m <= (1 << 26), "exl3_gemm needs 1 <= m <= 2^26");
     EXL3_CHECK(tiles_k > 0 && tiles_n > 0 && (tiles_k * 16) % 128 == 0 && (tiles_n * 16) % 128 == 0,
                "trellis dimensions must reconstruct whole 128-element Hadamard blocks");
-    EXL3_CHECK(tiles_k * 16 <= (1 << 24) && tiles_n * 16 <= (1 << 24), "feature dimensions too large");
+    EXL3_CHECK(tiles_k * 16 <= (1 << 20) && tiles_n * 16 <= (1 << 20), "feature dimensions too large");
     EXL3_CHECK(x && trellis && suh && svh && out, "null pointer argument");
     EXL3_CHECK(tiles_k * tiles_n * 32 * K < (1ll << 31), "packed trellis must be smaller than 2 GiB");
     const int64_t in_f = tiles_k * 16, out_f = tiles_n * 16;
+    const int64_t need = exl3_gemm_workspace_size(m, in_f, out_f);
+    EXL3_CHECK(workspace_bytes >= need && workspace, "workspace too small: need %lld bytes",
+               (long long)need);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (m >= linear_fat_min_rows())
+        return linear_fat(x, x_dtype, m, trellis, tiles_k, tiles_n, K, codebook, suh, svh, bias, bias_dtype,
+                          out, out_dtype, workspace, st);
     const LinPlan lp = plan_linear(m, in_f, out_f);
-    EXL3_CHECK(workspace_bytes >= (int64_t)lp.total && workspace,
-               "workspace too small: need %zu bytes", lp.total);
     uint16_t* img = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(workspace) + lp.off_img);
     RotateArgs ra = {};
     ra.x = x;
@@ -1598,13 +1639,14 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     p.out = out;
     p.out_dtype = out_dtype;
     p.out_stride = out_f;
+    p.bias = bias;
+    p.bias_dtype = bias_dtype;
     p.S = lp.ph.S;
     p.R_hb = lp.ph.R_hb;
     p.C_hb = lp.ph.C_hb;
     p.MRB = lp.MRB;
     p.n_rows_ws = (int)m;
     p.ws = reinterpret_cast<float*>(workspace);
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     profile_begin_call();
     profile_mark(0, st);
     const int64_t rot_units = m * (in_f / 128);
@@ -1615,12 +1657,23 @@ EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* tre
     profile_mark(2, st);
     if (lp.ph.S > 1) {
         const int items = (int)(m * (out_f / 128));
+        FinishBatch fb = {};
+        fb.bias = bias;
+        fb.bias_dtype = bias_dtype;
         linear_finish_kernel<<<(items + 3) / 4, 256, 0, st>>>(p.ws, lp.ph.S, (int)m, (int)out_f, svh,
-                                                              out, out_dtype, FinishBatch{});
+                                                              out, out_dtype, fb);
         EXL3_LAUNCHED();
         profile_mark(3, st);
     }
     return kOk;
+}
+
+EXL3_API int exl3_gemm(const void* x, int x_dtype, int64_t m, const int16_t* trellis,
+                       int64_t tiles_k, int64_t tiles_n, int64_t K, int codebook,
+                       const uint16_t* suh, const uint16_t* svh, void* out, int out_dtype,
+                       void* workspace, int64_t workspace_bytes, void* stream) {
+    return exl3_linear(x, x_dtype, m, trellis, tiles_k, tiles_n, K, codebook, suh, svh, nullptr, 0, out,
+                       out_dtype, workspace, workspace_bytes, stream);
 }
 
 struct BatchPlan {

@@ -100,6 +100,10 @@ struct GemvParams {
     int MRB;       // rows per row group (<= 16)
     int n_rows_ws; // rows addressed in the workspace (route rows or m)
     float* ws;
+    // Linear mode: optional bias [out_features] (bias_dtype as x_dtype ids),
+    // added after the output rotation.
+    const void* bias;
+    int bias_dtype;
     // Down mode: gate/up raw partials to finish while staging activations.
     const float* src_ws;
     int src_S;
@@ -270,6 +274,15 @@ __device__ __forceinline__ float load_act(const void* x, int dtype, int64_t idx)
         f = reinterpret_cast<const float*>(x)[idx];
     }
     return (float)f32_to_f16_rne(f);
+}
+
+// Element c of a bias vector (fp16 / bf16 / fp32); 0 without one.
+__device__ __forceinline__ float load_bias(const void* b, int dtype, int64_t c) {
+    if (!b) return 0.0f;
+    if (dtype == kF32) return reinterpret_cast<const float*>(b)[c];
+    const uint32_t h = reinterpret_cast<const uint16_t*>(b)[c];
+    if (dtype == kF16) return (float)bits_to_half(h);
+    return __builtin_bit_cast(float, h << 16);
 }
 
 __device__ __forceinline__ void store_out(void* out, int dtype, int64_t idx, float v) {

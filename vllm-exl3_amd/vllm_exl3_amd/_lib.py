@@ -28,6 +28,7 @@ SIGNATURES: dict[str, list] = {
     "exl3_decode_tiles": [_p, _i64, _i64, _i64, _i32, _p, _p],
     "exl3_gemm_workspace_size": [_i64, _i64, _i64],
     "exl3_gemm": [_p, _i32, _i64, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i32, _p, _i64, _p],
+    "exl3_linear": [_p, _i32, _i64, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i32, _p, _i32, _p, _i64, _p],
     "exl3_gemv_batched_workspace_size": [_i64, _i64, _i64, _i64],
     "exl3_gemv_batched": [_p, _i32, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i32, _p, _i32,
                           _p, _i64, _p],

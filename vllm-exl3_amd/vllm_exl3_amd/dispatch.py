@@ -235,9 +235,10 @@ class Exl3Linear:
         self.K, self.codebook = int(K), int(codebook)
 
     def forward(self, x: torch.Tensor, _params: dict | None = None, *,
-                out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+                out_dtype: torch.dtype = torch.float16,
+                bias: torch.Tensor | None = None) -> torch.Tensor:
         return C.exl3_gemm(x, self.trellis, self.suh, self.svh, self.K, True,
-                           codebook=self.codebook, out_dtype=out_dtype)
+                           codebook=self.codebook, out_dtype=out_dtype, bias=bias)
 
 
 def apply_exl3_python_loop(x2d: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,

@@ -158,21 +158,27 @@ def reserve_workspace(device: torch.device, kind: str, nbytes: int) -> torch.Ten
 # ---------------------------------------------------------------------------
 
 def _gemm_native(x2: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
-                 K: int, cb: int, out_dtype: torch.dtype) -> torch.Tensor:
+                 K: int, cb: int, out_dtype: torch.dtype,
+                 bias: torch.Tensor | None = None) -> torch.Tensor:
     dev = x2.device
     m, in_f = x2.shape
     out_f = trellis.size(1) * 16
     t = trellis.contiguous()
     su = suh.reshape(-1).contiguous()
     sv = svh.reshape(-1).contiguous()
+    b = None
+    if bias is not None:
+        _check(bias.numel() == out_f and bias.device == dev, "bias must hold out_features values on x's device")
+        b = bias.reshape(-1).contiguous()
     out = torch.empty((m, out_f), dtype=out_dtype, device=dev)
     lib = _lib.load()
     need = int(lib.exl3_gemm_workspace_size(m, in_f, out_f))
     ws = workspace(dev, "gemm", need)
     with torch.cuda.device(dev):
-        _lib.call("exl3_gemm", x2.data_ptr(), _dtype_id(x2, "x"), m, t.data_ptr(), t.size(0),
-                  t.size(1), K, cb, su.data_ptr(), sv.data_ptr(), out.data_ptr(),
-                  _DTYPE_ID[out_dtype], ws.data_ptr(), ws.numel(), stream_of(dev))
+        _lib.call("exl3_linear", x2.data_ptr(), _dtype_id(x2, "x"), m, t.data_ptr(), t.size(0),
+                  t.size(1), K, cb, su.data_ptr(), sv.data_ptr(),
+                  b.data_ptr() if b is not None else None, _dtype_id(b, "bias") if b is not None else 0,
+                  out.data_ptr(), _DTYPE_ID[out_dtype], ws.data_ptr(), ws.numel(), stream_of(dev))
     return out
 
 
@@ -211,15 +217,20 @@ def exl3_gemv(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: to
 
 def exl3_gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
               K: int, mcg: bool, *, mul1: bool = False, codebook: int | None = None,
-              out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
-    """Any-m EXL3 GEMM: fp16 [m, out].  csrc/bindings.cpp:110-115."""
+              out_dtype: torch.dtype = torch.float16, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Any-m EXL3 linear: [m, out] of out_dtype (fp16 by default, as the
+    reference).  csrc/bindings.cpp:110-115; from 128 rows the weights are
+    decoded once per 256 rows on MFMA (the reference's reconstruct + hgemm
+    route, src/vllm_exl3/exl3.py:5797-5819).  ``bias`` (keyword extension)
+    is added after the output rotation."""
     K = int(K)
     _check(x.dim() >= 1 and x.numel() > 0, "x must have shape [..., in_features]")
     _check_linear(x, trellis, suh, svh, K)
     cb = codebook_id(mcg, mul1, codebook)
     dev = _gpu_device(x)
     x2 = x.to(dev).contiguous().view(-1, x.size(-1))
-    out = _gemm_native(x2, trellis.to(dev), suh.to(dev), svh.to(dev), K, cb, out_dtype)
+    out = _gemm_native(x2, trellis.to(dev), suh.to(dev), svh.to(dev), K, cb, out_dtype,
+                       None if bias is None else bias.to(dev))
     return out if x.is_cuda else out.to(x.device)
 
 
