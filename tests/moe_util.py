@@ -53,7 +53,7 @@ def dense_of_layer(layer: dict, ks: list, cb: int):
     """dense(e) for a device layer built by synthetic.moe_layer_device: the
     expert's three projections dequantised on the GPU (the HIP dequant is
     pinned bit-exact to the oracle), one expert at a time to bound memory."""
-    store = layer["_store"]
+    store = layer["_store"][3:]  # after the whole-layer buffers: (trellis, suh, svh) per projection
 
     def dense(e):
         d = {}

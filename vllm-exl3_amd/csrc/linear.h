@@ -10,7 +10,7 @@ namespace exl3 {
 
 // Rows from which exl3_linear takes the fat path (measured crossover on
 // MI355X, bench.py --linear-crossover).
-constexpr int64_t kLinearFatMinRows = 128;
+constexpr int64_t kLinearFatMinRows = 256;
 
 size_t linear_fat_workspace_bytes(int64_t m, int64_t in_f, int64_t out_f);
 

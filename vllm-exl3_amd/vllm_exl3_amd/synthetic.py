@@ -154,38 +154,42 @@ def moe_layer_device(seed: int, n_experts: int, hidden: int, inter: int, K, devi
     """Like ``to_device(moe_layer(...))`` but generated on the device from
     ``DeviceBits`` (for multi-GB layers; the bits differ from the numpy
     generator's, the distributions are the same).  ``K`` is an int or a
-    per-expert sequence of ints."""
+    per-expert sequence of ints.  All trellis bits come from one fill and
+    all scales from a few whole-layer tensor ops, so a layer costs a handful
+    of kernel launches whatever its expert count."""
     import torch
 
     gen = DeviceBits(seed, device)
-
-    def bits(in_f, out_f, k):
-        n = (in_f // 16) * (out_f // 16) * 16 * k
-        return gen.words(n // 2).view(torch.int16).view(in_f // 16, out_f // 16, 16 * k)
-
-    def su(n):
-        return gen.signs(n).half()
-
-    def sv(n):
-        u = 0.005 + 0.015 * gen.uniform(n)
-        return (gen.signs(n) * u).half()
-
-    store = []
     names = ("gate", "up", "down")
-    tabs = {f"{p}_{a}": [] for p in names for a in ("trellis", "suh", "svh")}
-    ks = {p: [] for p in names}
+    ks = [int(K if isinstance(K, (int, np.integer)) else K[e]) for e in range(n_experts)]
+    shapes = []  # (expert, projection, in, out, K, trellis offset in int16, scale offsets)
+    t_off = s_off = v_off = 0
     for e in range(n_experts):
-        k = int(K if isinstance(K, (int, np.integer)) else K[e])
         for p in names:
             i_f, o_f = (hidden, inter) if p != "down" else (inter, hidden)
-            t, s_u, s_v = bits(i_f, o_f, k), su(i_f), sv(o_f)
-            store += [t, s_u, s_v]
-            tabs[f"{p}_trellis"].append(t.data_ptr())
-            tabs[f"{p}_suh"].append(s_u.data_ptr())
-            tabs[f"{p}_svh"].append(s_v.data_ptr())
-            ks[p].append(k)
+            n = (i_f // 16) * (o_f // 16) * 16 * ks[e]
+            shapes.append((e, p, i_f, o_f, ks[e], t_off, s_off, v_off))
+            t_off += n + (-n) % 128  # keep every projection 256-byte aligned
+            s_off += i_f
+            v_off += o_f
+    trellis_all = gen.words(t_off // 2).view(torch.int16)
+    suh_all = gen.signs(s_off).half()
+    svh_all = (gen.signs(v_off) * (0.005 + 0.015 * gen.uniform(v_off))).half()
+    tabs = {f"{p}_{a}": [] for p in names for a in ("trellis", "suh", "svh")}
+    store = [trellis_all, suh_all, svh_all]
+    kt = {p: [] for p in names}
+    for e, p, i_f, o_f, k, to, so, vo in shapes:
+        n = (i_f // 16) * (o_f // 16) * 16 * k
+        t = trellis_all[to:to + n].view(i_f // 16, o_f // 16, 16 * k)
+        su = suh_all[so:so + i_f]
+        sv = svh_all[vo:vo + o_f]
+        store += [t, su, sv]
+        tabs[f"{p}_trellis"].append(t.data_ptr())
+        tabs[f"{p}_suh"].append(su.data_ptr())
+        tabs[f"{p}_svh"].append(sv.data_ptr())
+        kt[p].append(k)
     out = {k: torch.tensor(v, dtype=torch.int64, device=device) for k, v in tabs.items()}
-    out["k_tables"] = tuple(torch.tensor(ks[p], dtype=torch.int8, device=device) for p in names)
+    out["k_tables"] = tuple(torch.tensor(kt[p], dtype=torch.int8, device=device) for p in names)
     out["_store"] = store
     return out
 
