@@ -27,7 +27,7 @@
 #include "gemv_core.h"
 #include "linear.h"
 #include "profile.h"
-#include "route.h"
+#include "route_impl.h"
 
 #include <cmath>
 #include <cstdlib>
@@ -232,10 +232,33 @@ __device__ __forceinline__ void finish_block(float& v0, float& v1, const uint16_
     v1 = v1 * kHadNorm * (float)bits_to_half(svh[c0 + 64]);
 }
 
-// Finish gate/up for one route row and one 128-block hb of the intermediate
-// dimension, and rotate the activation for the down projection.  g and u
-// leave the GEMV as fp16 and the activation is stored as fp16
+// The activation of one route row and 128-block hb of the intermediate
+// dimension from the summed raw gate (q 0) and up (q 1) results v[q][h]
+// (column hb*128 + lane + 64 h): rotation x svh, fp16, clamp + activation,
+// fp16, x down suh, rotation for the down projection.  g and u leave the
+// GEMV as fp16 and the activation is stored as fp16
 // (src/vllm_exl3/exl3.py:2403-2410, csrc/p2b_moe.cu:755-768).
+__device__ __forceinline__ void act_finish(float (&v)[2][2], const Proj* gu, int nproj,
+                                           const uint16_t* down_suh, int hb, int lane, int act,
+                                           float limit, float& a0, float& a1) {
+    const int c0 = hb * 128 + lane;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+        if (q < nproj) finish_block(v[q][0], v[q][1], gu[q].svh, c0, lane);
+    float a[2];
+    for (int h = 0; h < 2; ++h) {
+        const float u = (float)f32_to_f16_rne(nproj == 2 ? v[1][h] : v[0][h]);
+        const float g = nproj == 2 ? (float)f32_to_f16_rne(v[0][h]) : 0.0f;
+        a[h] = (float)f32_to_f16_rne(activate(g, u, act, limit));
+    }
+    a[0] *= (float)bits_to_half(down_suh[c0]);
+    a[1] *= (float)bits_to_half(down_suh[c0 + 64]);
+    had128(a[0], a[1], lane);
+    a0 = a[0] * kHadNorm;
+    a1 = a[1] * kHadNorm;
+}
+
+// Finish gate/up for one route row and 128-block hb from the split partials.
 __device__ __forceinline__ void gateup_finish(const GemvParams& p, const Proj* gu, int nproj,
                                               const uint16_t* down_suh, int64_t row, int hb,
                                               int lane, float& a0, float& a1) {
@@ -249,21 +272,9 @@ __device__ __forceinline__ void gateup_finish(const GemvParams& p, const Proj* g
                        (int64_t)p.n_rows_ws * inter, p.src_S, c0, v[q][0], v[q][1]);
         }
     }
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-        if (q < nproj) finish_block(v[q][0], v[q][1], gu[q].svh, c0, lane);
-    float a[2];
-    for (int h = 0; h < 2; ++h) {
-        const float u = (float)f32_to_f16_rne(nproj == 2 ? v[1][h] : v[0][h]);
-        const float g = nproj == 2 ? (float)f32_to_f16_rne(v[0][h]) : 0.0f;
-        a[h] = (float)f32_to_f16_rne(activate(g, u, p.act, p.limit));
-    }
-    a[0] *= (float)bits_to_half(down_suh[c0]);
-    a[1] *= (float)bits_to_half(down_suh[c0 + 64]);
-    had128(a[0], a[1], lane);
-    a0 = a[0] * kHadNorm;
-    a1 = a[1] * kHadNorm;
+    act_finish(v, gu, nproj, down_suh, hb, lane, p.act, p.limit, a0, a1);
 }
+
 
 // Position of input c of a row in the GEMV image: each 16 consecutive inputs
 // are stored in the MFMA k order of the GEMV (input c at pi_inv(c & 15)), so
@@ -764,7 +775,8 @@ __device__ __forceinline__ void wg_consume(WgStream<K>& rs, int wave, int lane, 
 // Everything one projection of one row group needs, shared by all waves.
 struct WgGroup {
     int rg, nr, arow, row_base, hb_first, j, tiles_n, expert;
-    const void* img;  // rotated activation rows of the streamed projection
+    const void* img;      // rotated activation rows of the streamed projection
+    const int* row_map;   // sorted row -> image row (null: the same row)
 };
 
 // Copy the rotated activations of a row group for tile rows [kt0, kt0 + nkt)
@@ -785,7 +797,8 @@ __device__ __forceinline__ void wg_stage_rows(const GemvParams& p, const WgGroup
             const int pc = b0 + b * kThreads + tid;
             if (pc < pieces) {
                 const int h = pc & 1, kt = (pc >> 1) % nkt, r = (pc >> 1) / nkt;
-                const int64_t row = G.row_base + G.rg + r;
+                const int64_t srow = G.row_base + G.rg + r;
+                const int64_t row = G.row_map ? G.row_map[srow] : srow;
                 v[b] = *(gv4c)(img + row * p.x_stride + (int64_t)(kt0 + kt) * 16 + 8 * h);
             }
         }
@@ -854,6 +867,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     const int s = (item / nsplit_proj) % p.S;
     const int rest = item / nsplit_proj / p.S;
     WgGroup G;
+    G.row_map = MODE == kModeGateUp ? p.row_map : nullptr;
     const int jb = rest % nJB;
     const int slot = rest / nJB;
 
@@ -1049,6 +1063,61 @@ __global__ __launch_bounds__(kThreads) void gemv_anyk_kernel(GemvParams p) {
                 dst[(int64_t)(rg + r) * p.out_features + c] = v;
             }
             __syncthreads();
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Routing and input rotation in one launch (decode steps whose gate/up phase
+// runs one unit per workgroup): block 0 routes (the stable multisplit sort
+// of route_impl.h) while the other blocks rotate every kept route's gate/up
+// input rows in route order; the GEMV stages a sorted row through the
+// router's sorted row -> route map.  Saves the rotation launch; the two
+// halves of the work never wait on each other.
+// ---------------------------------------------------------------------------
+struct RouteRotateArgs {
+    const void* ids;
+    int ids_i64, n_routes, topk, n_local, T, tile_rows;
+    const int32_t* n_valid;
+    const void* x;
+    int x_dtype, hidden;
+    const int64_t* suh_tab0;  // per-expert suh of the gate (or, gateless, up) projection
+    const int64_t* suh_tab1;  // per-expert suh of the up projection
+    int nproj;
+    uint16_t* img0;           // [n_routes][hidden] rotated rows, route order
+    uint16_t* img1;
+    RouteOut ro;
+};
+
+__global__ __launch_bounds__(kRouteThreads) void route_rotate_kernel(RouteRotateArgs f) {
+    if (blockIdx.x == 0) {
+        route_multisplit_body(f.ids, f.ids_i64, f.n_routes, f.topk, f.n_local, f.n_valid, f.tile_rows, f.ro);
+        return;
+    }
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t nb = blockIdx.x - 1, nblk = gridDim.x - 1;
+    const int live = f.n_valid ? min(f.T, max(0, f.n_valid[0])) : f.T;
+    const int64_t gw = nb * (kRouteThreads / 64) + (tid >> 6);
+    const int64_t nw = nblk * (kRouteThreads / 64);
+    const int nhb = f.hidden >> 7;
+    for (int64_t u = gw; u < (int64_t)f.n_routes * nhb; u += nw) {
+        const int64_t r = u / nhb;
+        const int hb = (int)(u % nhb);
+        const int64_t t = r / f.topk;
+        const int64_t e = f.ids_i64 ? reinterpret_cast<const int64_t*>(f.ids)[r]
+                                    : (int64_t)reinterpret_cast<const int32_t*>(f.ids)[r];
+        if (t >= live || e < 0 || e >= f.n_local) continue;  // wave-uniform: a dropped route
+        const int64_t fb = (int64_t)hb * 128;
+        const float x0 = load_act(f.x, f.x_dtype, t * f.hidden + fb + lane);
+        const float x1 = load_act(f.x, f.x_dtype, t * f.hidden + fb + lane + 64);
+        for (int q = 0; q < f.nproj; ++q) {
+            const uint16_t* su = reinterpret_cast<const uint16_t*>(q ? f.suh_tab1[e] : f.suh_tab0[e]);
+            float v0 = x0 * (float)bits_to_half(su[fb + lane]);
+            float v1 = x1 * (float)bits_to_half(su[fb + lane + 64]);
+            had128(v0, v1, lane);
+            uint16_t* dst = (q ? f.img1 : f.img0) + r * f.hidden;
+            dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0 * kHadNorm));
+            dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1 * kHadNorm));
         }
     }
 }
@@ -1429,10 +1498,17 @@ inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, i
     return best;
 }
 
+// EXL3_MOE_ROUTE_ROTATE=0 keeps routing and the input rotation in separate
+// launches (for comparisons; read on every call).
+inline bool moe_route_rotate_allowed() {
+    const char* v = std::getenv("EXL3_MOE_ROUTE_ROTATE");
+    return !(v && v[0] == '0');
+}
+
 struct MoePlan {
     int n_routes, max_slots, max_groups, MRB, nproj;
     PhasePlan gu, dn;
-    size_t off_route, off_wsgu, off_wsd, off_img, off_imgd, total;
+    size_t off_route, off_aux, off_wsgu, off_wsd, off_img, off_imgd, total;
 };
 
 inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden, int64_t inter,
@@ -1460,6 +1536,8 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
     m.off_route = off;
     off += align256(sizeof(int) * (2 + 3 * (size_t)m.max_slots + 3 * (size_t)m.n_routes +
                                    3 * (size_t)m.max_groups));
+    m.off_aux = off;  // sorted row -> route [routes]
+    off += align256(sizeof(int) * (size_t)m.n_routes);
     m.off_wsgu = off;
     off += align256(4 * (size_t)m.nproj * m.gu.S * m.n_routes * inter);
     m.off_wsd = off;
@@ -1841,7 +1919,48 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     ro.mt_slot = ro.n_mtiles + 1;
     ro.mt_row0 = ro.mt_slot + mp.max_groups;
     ro.mt_expert = ro.mt_row0 + mp.max_groups;
-    if (n_local <= kRouteMaxLocal) {
+    const int64_t* tabs[9] = {gateless ? up_trellis : gate_trellis, gateless ? up_suh : gate_suh,
+                              gateless ? up_svh : gate_svh, up_trellis, up_suh, up_svh,
+                              down_trellis, down_suh, down_svh};
+    uint16_t* img_gu = reinterpret_cast<uint16_t*>(ws + mp.off_img);
+    uint16_t* img_gu1 = img_gu + (size_t)mp.n_routes * hidden;
+    // Route and rotate in one launch when the gate/up GEMV stages its rows
+    // through the sorted row -> route map (one unit per workgroup, uniform K).
+    const bool route_rotate = moe_route_rotate_allowed() && mp.gu.wg && n_local <= kRouteMaxLocal &&
+                              !kt[0] && !kt[1];
+    if (route_rotate) {
+        static const hipError_t attr = [] {
+            hipError_t e = hipFuncSetAttribute((const void*)route_rotate_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)route_lds_bytes(kRouteMaxLocal));
+            if (e != hipSuccess) (void)hipGetLastError();
+            return e;
+        }();
+        EXL3_HIP(attr);
+        ro.row_route = reinterpret_cast<int*>(ws + mp.off_aux);
+        RouteRotateArgs f = {};
+        f.ids = ids;
+        f.ids_i64 = (int)ids_dtype;
+        f.n_routes = mp.n_routes;
+        f.topk = (int)topk;
+        f.n_local = (int)n_local;
+        f.T = (int)T;
+        f.tile_rows = mp.MRB;
+        f.n_valid = n_valid;
+        f.x = x;
+        f.x_dtype = (int)x_dtype;
+        f.hidden = (int)hidden;
+        f.suh_tab0 = tabs[1];
+        f.suh_tab1 = tabs[4];
+        f.nproj = mp.nproj;
+        f.img0 = img_gu;
+        f.img1 = img_gu1;
+        f.ro = ro;
+        const int64_t units = (int64_t)mp.n_routes * (hidden / 128);
+        const int64_t rot_blocks = std::min<int64_t>((units + kRouteThreads / 64 - 1) / (kRouteThreads / 64), 1024);
+        route_rotate_kernel<<<(unsigned)(1 + rot_blocks), kRouteThreads, route_lds_bytes((int)n_local), st>>>(f);
+        EXL3_LAUNCHED();
+    } else if (n_local <= kRouteMaxLocal) {
         EXL3_HIP(launch_route(ids, ids_dtype, mp.n_routes, (int)topk, (int)n_local, n_valid, mp.MRB, ro,
                               st));
     } else {
@@ -1851,9 +1970,6 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     }
 
     GemvParams p = {};
-    const int64_t* tabs[9] = {gateless ? up_trellis : gate_trellis, gateless ? up_suh : gate_suh,
-                              gateless ? up_svh : gate_svh, up_trellis, up_suh, up_svh,
-                              down_trellis, down_suh, down_svh};
     for (int i = 0; i < 9; ++i) p.tab[i] = tabs[i];
     for (int i = 0; i < 3; ++i) {
         p.ktab[i] = kt[i];
@@ -1877,33 +1993,35 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     p.act = act;
     float* ws_gu = reinterpret_cast<float*>(ws + mp.off_wsgu);
     float* ws_d = reinterpret_cast<float*>(ws + mp.off_wsd);
-    uint16_t* img_gu = reinterpret_cast<uint16_t*>(ws + mp.off_img);
     uint16_t* img_d = reinterpret_cast<uint16_t*>(ws + mp.off_imgd);
 
     // gate/up input rows, rotated once per route and projection
     profile_mark(1, st);
-    RotateArgs ra = {};
-    ra.x = x;
-    ra.x_dtype = x_dtype;
-    ra.x_stride = hidden;
-    ra.in_f = (int)hidden;
-    ra.n_rows = mp.n_routes;
-    ra.route_pos = ro.route_pos;
-    ra.topk = (int)topk;
-    ra.row_expert = ro.row_expert;
-    ra.suh_tab[0] = tabs[1];
-    ra.suh_tab[1] = tabs[4];
-    ra.nproj = mp.nproj;
-    ra.img[0] = img_gu;
-    ra.img[1] = img_gu + (size_t)mp.n_routes * hidden;
-    const int64_t gu_units = (int64_t)mp.n_routes * (hidden / 128);
-    rotate_rows_kernel<<<(unsigned)((gu_units + 3) / 4), 256, 0, st>>>(ra);
-    EXL3_LAUNCHED();
+    if (!route_rotate) {
+        RotateArgs ra = {};
+        ra.x = x;
+        ra.x_dtype = x_dtype;
+        ra.x_stride = hidden;
+        ra.in_f = (int)hidden;
+        ra.n_rows = mp.n_routes;
+        ra.route_pos = ro.route_pos;
+        ra.topk = (int)topk;
+        ra.row_expert = ro.row_expert;
+        ra.suh_tab[0] = tabs[1];
+        ra.suh_tab[1] = tabs[4];
+        ra.nproj = mp.nproj;
+        ra.img[0] = img_gu;
+        ra.img[1] = img_gu1;
+        const int64_t gu_units = (int64_t)mp.n_routes * (hidden / 128);
+        rotate_rows_kernel<<<(unsigned)((gu_units + 3) / 4), 256, 0, st>>>(ra);
+        EXL3_LAUNCHED();
+    }
 
     // gate/up: raw partial sums [nproj][S_gu][routes][inter]
     GemvParams pg = p;
-    pg.x = ra.img[0];
-    pg.x2 = ra.img[1];
+    pg.x = img_gu;
+    pg.x2 = img_gu1;
+    pg.row_map = route_rotate ? ro.row_route : nullptr;
     pg.x_dtype = kF16;
     pg.x_stride = hidden;
     pg.in_features = (int)hidden;

@@ -104,6 +104,10 @@ struct GemvParams {
     // added after the output rotation.
     const void* bias;
     int bias_dtype;
+    // GateUp mode, one unit per workgroup: sorted row -> activation image row
+    // (images written in route order by the combined route + rotate launch);
+    // null: the image rows are the sorted rows.
+    const int* row_map;
     // Down mode: gate/up raw partials to finish while staging activations.
     const float* src_ws;
     int src_S;

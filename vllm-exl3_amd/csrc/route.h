@@ -22,6 +22,7 @@ struct RouteOut {
     int* mt_row0;      // [max_mtiles]
     int* n_sorted;     // [1] routes kept (nullable)
     int* mt_expert;    // [max_mtiles] local expert of each row tile (nullable)
+    int* row_route;    // [n_routes]: sorted row -> route (nullable)
 };
 
 // Upper bound of the row tiles produced for tile_rows-row tiles.
