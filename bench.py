@@ -506,6 +506,63 @@ def kv_decode_c4(S, torch, dev, steps, warmup, PhaseTimer):
     }
 
 
+# The reference's published per-layer prefill times with the fast q4 staging
+# and without staging (unquantised cache), GB10 (CHECKIN-Q4KV-1.md:1227-1235
+# of the reference): the staging share is their difference.
+Q4_REF_PREFILL_MS = {8192: (4.42, 3.99), 16384: (4.45, 4.31), 30720: (5.89, 4.83)}
+Q4_STAGE_CAP = 192  # staging rows: 48 MiB at 4 KV heads (the reference's default cap)
+
+
+def q4_stage_prefill(S, torch, dev, steps, warmup, PhaseTimer):
+    """q4 prefill staging (q4_stage_pages) of an 8K / 16K / 30K-token prefix
+    at the reference harness's 4 KV heads: every page of the prefix staged
+    once, in slices of at most Q4_STAGE_CAP - 1 pages (one launch each),
+    from a pool of 256 pages in a random page order."""
+    from vllm_exl3_amd import nvfp4_kv as Q
+
+    H, n_pool = 4, 256
+    L = n_pool * 128
+    k, v = S.kv_inputs_device(7, 1, H, L, dev)
+    bt = torch.from_numpy(S.block_table(7, 1, n_pool)).to(dev)
+    pool = Q.new_pool(n_pool, H, dev)
+    Q.pack_pages(k, v, torch.tensor([L], dtype=torch.int32, device=dev), bt, pool)
+    del k, v
+    buf = torch.empty((Q4_STAGE_CAP, H, 128, 256), dtype=torch.bfloat16, device=dev)
+    page_bytes = H * (2 * 9216 + 128 * 256 * 2)  # read both slots, write the K|V row
+    out = {}
+    for prefix, (ref_fast, ref_none) in Q4_REF_PREFILL_MS.items():
+        nb = prefix // 128
+        pages = bt[0, :nb].to(torch.int64)
+        slices = [pages[i:i + Q4_STAGE_CAP - 1] for i in range(0, nb, Q4_STAGE_CAP - 1)]
+
+        def call():
+            for sl in slices:
+                Q.q4_stage_pages(buf, pool, sl)
+
+        ev = event_stats(torch, call, steps, warmup)
+        torch.cuda.synchronize()
+        with PhaseTimer(max_calls=steps * len(slices)) as pt:
+            for _ in range(steps):
+                call()
+            torch.cuda.synchronize()
+        kern_us = pt.mean_ms(0) * 1e3 * len(slices)  # phase 0 is one launch; means are per launch
+        nbytes = nb * page_bytes + len(slices) * H * 128 * 256 * 2
+        out[f"{prefix // 1024}K"] = {
+            "pages": nb, "slices": len(slices),
+            "call_us": round(ev["median_ms"] * 1e3, 2), "p95_us": round(ev["p95_ms"] * 1e3, 2),
+            "kernel_us": round(kern_us, 2),
+            "kernel_gbs": round(nbytes / (kern_us * 1e-6) / 1e9, 1),
+            "frac_hbm_peak": round(nbytes / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes": nbytes,
+            "ref_gb10_prefill_ms_fast_vs_unstaged": [ref_fast, ref_none],
+            "ref_gb10_staging_share_ms": round(ref_fast - ref_none, 2),
+        }
+    del pool, buf
+    return {"workload": "q4 prefill staging (q4_stage_pages), 4 KV heads, 128-token pages, "
+                        "prefix pages in random pool order",
+            "per_prefix": out}
+
+
 def crossover(args) -> int:
     """Median µs per call of moe_forward (decode executor) and moe_prefill
     (prefill executor) for T tokens, softmax top-8 routing, on two layer
@@ -584,8 +641,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=5,
                     help="distinct C1 layers the decode steps rotate over (HBM-resident weights)")
-    ap.add_argument("--configs", default="c0,c2,c3,c4",
-                    help="other BASELINE configs reported beside the headline (c0,c2,c3,c4; '' = none)")
+    ap.add_argument("--configs", default="c0,c2,c3,c4,q4",
+                    help="other BASELINE configs reported beside the headline (c0,c2,c3,c4 and q4, the "
+                         "q4 prefill staging; '' = none)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
@@ -722,6 +780,8 @@ def main() -> int:
         line["mixed_k_c3"] = decode_c3(C, S, torch, dev, args.steps, args.warmup, PhaseTimer)
     if "c4" in others:
         line["kv_decode_c4"] = kv_decode_c4(S, torch, dev, args.steps, args.warmup, PhaseTimer)
+    if "q4" in others:
+        line["q4_stage"] = q4_stage_prefill(S, torch, dev, args.steps, args.warmup, PhaseTimer)
     if not args.no_cpu_baseline:
         import oracle as O
 

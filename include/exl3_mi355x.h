@@ -279,6 +279,17 @@ int exl3_nvfp4_pack_pages(const void* k, const void* v, int dtype, int64_t B, in
                           int64_t max_blocks, void* pool, int64_t num_pages, void* stream);
 int exl3_nvfp4_dequant_pages(const void* pool, int64_t num_pages, int64_t H, float* out,
                              void* stream);
+/* Prefill staging: page list -> bf16 staging rows.  stage is bf16
+ * [capacity][H][128][256] (contiguous): row r < n holds page pages[r]
+ * (int32 when pages_dtype is 0, int64 when 1), K values in columns 0..127
+ * and V values in 128..255, bit-identical to the bf16 cast of the fp32 pool
+ * dequant (every e2m1 x e4m3 product is exact in bf16; a NaN scale code
+ * gives 0x7FC0); row n is zeroed, as is a row whose page id lies outside
+ * [0, num_pages).  Requires n + 1 <= capacity.  No host synchronisation.
+ * Replaces q4_stage_pages + _q4_stage_kernel
+ * (src/vllm_exl3/minimax_q4kv_kernels.py:509-566, 880-951). */
+int exl3_nvfp4_stage_pages(const void* pool, int64_t num_pages, int64_t H, const void* pages,
+                           int pages_dtype, int64_t n, void* stage, int64_t capacity, void* stream);
 int64_t exl3_nvfp4_decode_workspace_size(int64_t total_q, int64_t Hq, int64_t n_chunks);
 int exl3_nvfp4_sparse_decode(const void* q, int q_dtype, int64_t total_q, int64_t Hq, int64_t Hkv,
                              int64_t q_stride_n, int64_t q_stride_h, const void* pool,

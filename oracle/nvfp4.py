@@ -14,7 +14,8 @@ relative to the vllm-exl3 repository root):
   (``:140-154``);
 * RZ of the exact product at fp32 precision (``:256-294``);
 * row pack / unpack (``:297-349``), slot-region pack (``:352-366``), pool
-  dequant (``:735-776``);
+  dequant (``:735-776``) and the bf16 prefill staging rows built from it
+  (``q4_stage_pages``, ``minimax_q4kv_kernels.py:509-566, 880-951``);
 * block-sparse decode attention over top-k pages with the causal rule of
   the decode kernel (``minimax_q4kv_kernels.py:416-506``), in float64, with
   the union-of-blocks semantics of ``reference_sparse_attention``
@@ -213,6 +214,38 @@ def dequant_pool(pool) -> np.ndarray:
     for p in range(P):
         for s in range(S):
             out[p, s] = unpack_slot(pool[p, s], s % 2)
+    return out
+
+
+def bf16_bits(x) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, RNE; NaN -> 0x7FC0 (torch's scalar
+    float -> bfloat16 cast)."""
+    x = np.asarray(x, dtype=np.float32)
+    b = x.view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(np.isnan(x), np.uint16(0x7FC0), r).astype(np.uint16)
+
+
+def stage_pages(pool, pages, capacity: int | None = None) -> np.ndarray:
+    """Prefill staging (``q4_stage_pages``, ``minimax_q4kv_kernels.py:880-951``,
+    kernel ``:509-566``): bf16 bits [capacity or n+1, Hkv, 128, 256]; row r
+    < n holds page pages[r] -- the bf16 cast of ``dequant_pool`` with the K
+    slot (2h) in columns 0..127 and the V slot (2h+1) in 128..255 -- and every
+    other row is zero, as is a row whose page id is outside [0, nb) (this
+    build's definition; the reference kernel does not bound the id)."""
+    pool = np.asarray(pool, dtype=np.uint8)
+    nb, slots = pool.shape[:2]
+    pool = pool.reshape(nb, slots, SLOT_REGION)
+    H = slots // 2
+    pages = np.asarray(pages, dtype=np.int64).reshape(-1)
+    n = pages.size
+    rows = n + 1 if capacity is None else capacity
+    out = np.zeros((rows, H, PAGE_TOKENS, 2 * HEAD_DIM), np.uint16)
+    for r, pg in enumerate(pages):
+        if 0 <= pg < nb:
+            vals = dequant_pool(pool[pg:pg + 1])[0]          # [2H, 128, 128]
+            out[r, :, :, :HEAD_DIM] = bf16_bits(vals[0::2])
+            out[r, :, :, HEAD_DIM:] = bf16_bits(vals[1::2])
     return out
 
 

@@ -6,7 +6,12 @@
 * the e4m3 encoder against torch's float8_e4m3fn cast (a library routine);
 * byte fixtures written by the reference's own packer
   (tests/golden/make_nvfp4_vectors.py) incl. ties, RZ boundaries,
-  saturation, clamped and zero groups.
+  saturation, clamped and zero groups;
+* the prefill staging rows: exactness of every e2m1 x e4m3 product in bf16
+  (all 16 x 256 codes), the identity on rows the format holds exactly
+  (pack -> stage gives the rows back, K and V halves), the zero row and the
+  reference test's layout (tests/test_minimax_q4kv.py:560-581 of the
+  reference).
 """
 
 import pathlib
@@ -235,3 +240,71 @@ def test_w1_write_layout():
     assert not icache[3].any()
     ikn = N.rope_partial_neox(N.gemma_rmsnorm(x[:, -1], ws[3], eps), csr, W1_ROT)
     assert np.array_equal(icache[[0, 1, 2, 4]], N.e4m3_clamped(ikn)[[0, 1, 2, 4]])
+
+
+def test_stage_products_exact_in_bf16():
+    """Every e2m1 x e4m3 product is a bf16 value: staging is a lossless cast."""
+    e2 = N.e2m1_decode(np.arange(16))
+    e4 = N.e4m3_decode(np.arange(256))
+    prod = (e2[:, None] * e4[None, :]).astype(np.float32)
+    bits = N.bf16_bits(prod)
+    finite = np.isfinite(prod)
+    back = (bits.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(back[finite].view(np.uint32), prod[finite].view(np.uint32))
+    assert (bits[~finite] == 0x7FC0).all() and (~finite).sum() == 2 * 16
+
+
+def _representable_rows(rng, n):
+    """Rows the q4 format holds exactly: per 16-group a power-of-two scale s
+    and e2m1 multiples of s with one +-6 s (so amax / 6 == s)."""
+    s = np.exp2(rng.integers(-6, 4, size=(n, 8))).astype(np.float32)
+    codes = rng.integers(0, 16, size=(n, 8, 16))
+    codes[:, :, 0] = np.where(rng.random((n, 8)) < 0.5, 7, 15)  # +-6
+    vals = N.e2m1_decode(codes) * s[:, :, None]
+    return vals.reshape(n, 128).astype(np.float32)
+
+
+def test_stage_pages_identity_on_representable_rows():
+    rng = np.random.default_rng(5)
+    H, nb = 3, 4
+    rows = _representable_rows(rng, nb * 2 * H * 128).reshape(nb, 2 * H, 128, 128)
+    pool = np.stack([np.stack([N.pack_slot(rows[p, sl], sl % 2) for sl in range(2 * H)])
+                     for p in range(nb)])
+    pages = np.array([2, 0, 3, 2])
+    st = N.stage_pages(pool, pages)
+    assert st.shape == (5, H, 128, 256) and not st[4].any()
+    as_f = (st.astype(np.uint32) << 16).view(np.float32)
+    for r, pg in enumerate(pages):
+        assert np.array_equal(as_f[r, :, :, :128], rows[pg, 0::2])   # K slots 2h
+        assert np.array_equal(as_f[r, :, :, 128:], rows[pg, 1::2])   # V slots 2h+1
+
+
+def test_stage_pages_layout_matches_reference_test():
+    """Reference tests/test_minimax_q4kv.py:560-581: staged[row, :, :, :128]
+    is the K page and [..., 128:] the V page, in bf16; the last row is zero;
+    capacity rows beyond n + 1 stay zero; an id outside the pool stages
+    zeros."""
+    rng = np.random.default_rng(6)
+    H, nb = 2, 3
+    x = N.bf16_round(rng.standard_normal((nb, 2 * H, 128, 128)).astype(np.float32))
+    pool = np.stack([np.stack([N.pack_slot(x[p, sl], sl % 2) for sl in range(2 * H)])
+                     for p in range(nb)])
+    vals = N.dequant_pool(pool)
+    st = N.stage_pages(pool.reshape(nb, 2 * H, 128, 72), [1, 7, 0], capacity=6)
+    assert st.shape == (6, H, 128, 256)
+    as_f = (st.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(as_f[0, :, :, :128], vals[1, 0::2])
+    assert np.array_equal(as_f[0, :, :, 128:], vals[1, 1::2])
+    assert np.array_equal(as_f[2, :, :, 128:], vals[0, 1::2])
+    assert not st[1].any() and not st[3:].any()
+
+
+def test_stage_pages_planted_side_swap_is_caught():
+    """A staging that puts the V slot first fails the identity check."""
+    rng = np.random.default_rng(7)
+    rows = _representable_rows(rng, 2 * 128).reshape(1, 2, 128, 128)
+    pool = np.stack([np.stack([N.pack_slot(rows[0, sl], sl % 2) for sl in range(2)])])
+    st = N.stage_pages(pool, [0])
+    swapped = np.concatenate([st[..., 128:], st[..., :128]], axis=-1)
+    as_f = (swapped.astype(np.uint32) << 16).view(np.float32)
+    assert not np.array_equal(as_f[0, 0, :, :128], rows[0, 0])

@@ -328,6 +328,56 @@ __global__ __launch_bounds__(256) void q4_dequant_kernel(const uint8_t* pool, in
     o[1] = (float)v[1] * sc;
 }
 
+// Prefill staging (q4_stage_pages / _q4_stage_kernel,
+// src/vllm_exl3/minimax_q4kv_kernels.py:509-566, 880-951): staged row r of
+// the bf16 buffer [rows][H][128 tokens][256] holds page pages[r] of the pool,
+// K values in columns 0..127 and V values in 128..255 (e2m1 x e4m3 in fp32,
+// then bf16; the product has at most 7 significant bits and lies inside
+// bf16's normal range, so the bf16 value is exact; a NaN scale code gives
+// 0x7FC0).  Row n (one past the last page) is written as zeros, and so is a
+// row whose page id is outside [0, num_pages).
+//
+// One thread per 8 consecutive output columns of one token: one 4-byte data
+// load, one scale byte, one 16-byte store; a workgroup covers 8 tokens x 256
+// columns of one (row, head), so each store instruction of a wave writes
+// 1 KiB of consecutive bytes.  Grid (rows, H, 16).
+constexpr int kStageTokPerBlock = 8;
+
+__global__ __launch_bounds__(256) void q4_stage_kernel(const uint8_t* pool, int64_t num_pages, int H,
+                                                       const void* pages, int pages_i64, int n,
+                                                       uint16_t* stage) {
+    const int row = blockIdx.x, head = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int t = blockIdx.z * kStageTokPerBlock + (tid >> 5);
+    const int col = (tid & 31) * 8;  // 0..248
+    const int side = col >> 7, d0 = col & 127;
+    int64_t page = -1;
+    if (row < n)
+        page = pages_i64 ? reinterpret_cast<const int64_t*>(pages)[row]
+                         : (int64_t)reinterpret_cast<const int32_t*>(pages)[row];
+    u32x4 o = {0u, 0u, 0u, 0u};
+    if (page >= 0 && page < num_pages) {
+        const uint8_t* region = pool + (page * 2 * H + 2 * head + side) * (int64_t)kQ4Slot;
+        const uint32_t d = *reinterpret_cast<const uint32_t*>(region + t * 64 + (d0 >> 1));
+        const float sc = e4m3_value(region[kQ4Data + scale_offset(side, t, d0 >> 4)]);
+        if (sc != sc) {
+            o = u32x4{0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u};
+        } else {
+            const h2v v[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 0),
+                              __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 1),
+                              __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 2),
+                              __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 3)};
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t lo = __builtin_bit_cast(uint32_t, bf16_round((float)v[b][0] * sc)) >> 16;
+                const uint32_t hi = __builtin_bit_cast(uint32_t, bf16_round((float)v[b][1] * sc)) >> 16;
+                o[b] = lo | (hi << 16);
+            }
+        }
+    }
+    *reinterpret_cast<u32x4*>(stage + (((int64_t)row * H + head) * kQ4Page + t) * 256 + col) = o;
+}
+
 struct Q4DecodeParams {
     const void* q;
     int q_dtype;
@@ -588,6 +638,26 @@ EXL3_API int exl3_nvfp4_dequant_pages(const void* pool, int64_t num_pages, int64
     q4_dequant_kernel<<<(unsigned)((bytes + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
         reinterpret_cast<const uint8_t*>(pool), n_slots, out);
     EXL3_LAUNCHED();
+    return kOk;
+}
+
+EXL3_API int exl3_nvfp4_stage_pages(const void* pool, int64_t num_pages, int64_t H, const void* pages,
+                                    int pages_dtype, int64_t n, void* stage, int64_t capacity,
+                                    void* stream) {
+    EXL3_CHECK(num_pages >= 1 && H >= 1 && H <= 65535 && pool && stage, "q4 staging: bad arguments");
+    EXL3_CHECK(pages_dtype == 0 || pages_dtype == 1, "q4 staging: page ids are int32 (0) or int64 (1)");
+    EXL3_CHECK(n >= 0 && (n == 0 || pages), "q4 staging: bad page list");
+    EXL3_CHECK(n + 1 <= capacity, "staging buffer holds %lld pages, need %lld", (long long)(capacity - 1),
+               (long long)n);
+    EXL3_CHECK(n < (1ll << 31) - 1, "q4 staging: too many pages");
+    const dim3 grid((unsigned)(n + 1), (unsigned)H, kQ4Page / kStageTokPerBlock);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    profile_begin_call();
+    profile_mark(0, st);
+    q4_stage_kernel<<<grid, 256, 0, st>>>(reinterpret_cast<const uint8_t*>(pool), num_pages, (int)H, pages,
+                                          pages_dtype, (int)n, reinterpret_cast<uint16_t*>(stage));
+    EXL3_LAUNCHED();
+    profile_mark(1, st);
     return kOk;
 }
 

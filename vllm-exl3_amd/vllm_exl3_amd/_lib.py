@@ -56,6 +56,7 @@ SIGNATURES: dict[str, list] = {
     "exl3_nvfp4_pack_pages": [_p, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64,
                               _p, _i64, _p],
     "exl3_nvfp4_dequant_pages": [_p, _i64, _i64, _p, _p],
+    "exl3_nvfp4_stage_pages": [_p, _i64, _i64, _p, _i32, _i64, _p, _i64, _p],
     "exl3_nvfp4_decode_workspace_size": [_i64, _i64, _i64],
     "exl3_nvfp4_sparse_decode": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64,
                                  _i64, _p, _i64, _i64, _p, _i64, _f32, _p, _i32, _i64, _i64, _i64,

@@ -1,5 +1,5 @@
 """The reference's NVFP4 ("q4") paged KV cache on the GPU: pack, pool
-dequant and the block-sparse decode attention.
+dequant, prefill staging and the block-sparse decode attention.
 
 Host side of ``q4_sparse_decode`` (src/vllm_exl3/minimax_q4kv_kernels.py:
 772-877) and of the reference packer / dequantiser
@@ -83,6 +83,58 @@ def dequant_pool_pages(pool: torch.Tensor) -> torch.Tensor:
         _lib.call("exl3_nvfp4_dequant_pages", pool.data_ptr(), pool.size(0), pool.size(1) // 2,
                   out.data_ptr(), stream_of(pool.device))
     return out
+
+
+def q4_stage_pages(buffer: torch.Tensor, pool: torch.Tensor, pages: torch.Tensor) -> int:
+    """Dequantise ``pages`` of the q4 pool into staging rows ``buffer[:n]``
+    and zero ``buffer[n]``; returns n = ``pages.numel()``.
+
+    Same arguments, result and refusals as ``q4_stage_pages``
+    (src/vllm_exl3/minimax_q4kv_kernels.py:880-951): ``buffer`` bf16
+    [capacity, num_kv_heads, 128, 256] (K values in columns 0..127, V values
+    in 128..255), ``pool`` uint8 [nb, 2*num_kv_heads, 128, 72] with
+    contiguous 9216-byte slot regions, ``pages`` int32/int64 physical page
+    ids.  The staged bytes equal the bf16 cast of ``dequant_pool_pages``
+    (every e2m1 x e4m3 product is exact in bf16).  One launch, which also
+    writes the zero row; page ids are read on the device only, so nothing
+    synchronises with the host.  A page id outside [0, nb) stages a row of
+    zeros."""
+    for name, t in (("buffer", buffer), ("pages", pages)):
+        if t.device != pool.device:
+            raise ValueError(f"q4 KV refused: '{name}' is on {t.device}, expected {pool.device}")
+    if not pool.is_cuda:
+        raise ValueError(f"q4 KV refused: 'pool' must be on a cuda device, got {pool.device}")
+    if pool.dtype is not torch.uint8:
+        raise ValueError("q4 staging requires the pool as raw uint8 bytes, got "
+                         f"{str(pool.dtype).replace('torch.', '')}; the overlay must re-view the "
+                         "container before dispatch")
+    if pool.dim() != 4 or pool.shape[2] != PAGE_TOKENS or pool.shape[3] != ROW_BYTES:
+        raise ValueError("q4 pool must be [nb, 2*num_kv_heads, 128, 72]")
+    if pool.stride(2) != ROW_BYTES or pool.stride(1) != PAGE_TOKENS * ROW_BYTES or pool.stride(3) != 1:
+        raise ValueError("q4 pool slot regions must be contiguous")
+    if buffer.dtype is not torch.bfloat16:
+        raise ValueError(f"staging buffer must be bf16, got {str(buffer.dtype).replace('torch.', '')}")
+    if pages.dtype not in (torch.int64, torch.int32):
+        raise ValueError(f"page ids must be int64/int32, got {str(pages.dtype).replace('torch.', '')}")
+    num_kv_heads = pool.shape[1] // 2
+    if buffer.dim() != 4 or buffer.shape[1] != num_kv_heads or buffer.shape[2] != PAGE_TOKENS \
+            or buffer.shape[3] != 256:
+        raise ValueError("staging buffer must be [capacity, num_kv_heads, 128, 256]")
+    if not buffer.is_contiguous():
+        raise ValueError("staging buffer must be contiguous")
+    n = int(pages.numel())
+    if n > buffer.shape[0] - 1:
+        raise ValueError(f"staging buffer holds {buffer.shape[0] - 1} pages, need {n}")
+    if pool.stride(0) != pool.shape[1] * PAGE_TOKENS * ROW_BYTES:
+        pool = pool.contiguous()
+    pg = pages.reshape(-1)
+    if n and not pg.is_contiguous():
+        pg = pg.contiguous()
+    with torch.cuda.device(pool.device):
+        _lib.call("exl3_nvfp4_stage_pages", pool.data_ptr(), pool.size(0), num_kv_heads,
+                  pg.data_ptr() if n else 0, 1 if pg.dtype == torch.int64 else 0, n, buffer.data_ptr(),
+                  buffer.size(0), stream_of(pool.device))
+    return n
 
 
 def _chunks(total_q: int, num_kv_heads: int, max_topk: int) -> int:
