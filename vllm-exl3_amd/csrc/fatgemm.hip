@@ -150,11 +150,16 @@ struct PairGeom {
 __device__ __forceinline__ int swz(int r, int c) { return r * 64 + (((c ^ (r >> 2) ^ (r >> 3)) & 3) << 4); }
 
 // LDS-only barrier: the stage buffers are handed over through LDS, and the
-// global prefetches must stay in flight across it.
+// global prefetches must stay in flight across it.  The scheduling barriers
+// keep the compiler from hoisting the next k-step's decode arithmetic above
+// it: that arithmetic reads the registers loaded last, so hoisting it turns
+// the two-step prefetch into a wait for the newest loads (vmcnt(0)).
 __device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 struct FatTile {
@@ -615,7 +620,8 @@ __global__ __launch_bounds__(256) void linear_out_kernel(const float* z, int N, 
 // per thread; each trellis group is decoded by two threads, one per column
 // half (waves 0-3 take half 0, waves 4-7 half 1, so the choice is uniform
 // per wave).
-constexpr int kFatThreads = 512;
+constexpr int kFatThreads = 768;
+constexpr int kFatProducers = 4;  // waves that load, decode and stage; the other eight run the MFMAs
 constexpr int kStages = 3;
 constexpr int kFatLds = kStages * (kABytes + kBBytes);  // 96 KB
 
@@ -634,26 +640,23 @@ __device__ __forceinline__ void decode_group_half(const uint32_t (&w)[K + 1], ui
     }
 }
 
-template <int CB, int K, int MF>
-__device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, uint8_t* lds) {
+// Producer waves (0..3, one per SIMD): global loads of A rows and packed
+// bits two k-steps ahead of their staging; per k-step each thread stages 64
+// bytes of A and decodes one 32-weight group (both column halves) into the
+// B stage.  One barrier per k-step, three stages, as the consumers.
+template <int CB, int K>
+__device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps) {
     constexpr int tile_bytes = 32 * K;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = w & 1, wn = w >> 1;
-    const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
+    const int pt = (threadIdx.x >> 6) / 3 * 64 + (threadIdx.x & 63);  // 0..255
     const int tiles_n = p.N >> 4;
-
-    // ---- staging roles
-    const int ac = tid & 3, ar0 = tid >> 2;  // A: chunk ac of rows ar0 and ar0 + 128
+    const int ac = pt & 3, ar0 = pt >> 2;  // A: chunk ac of rows ar0 + 64 jj
     const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.a + ft.a_row0 * p.lda), (short)0, 0x7FFFFFFF, 0x00020000);
-    int a_voff[2];
+    int a_voff[4];
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-        a_voff[jj] = (int)((min(ar0 + 128 * jj, ft.rows_valid - 1) * p.lda + 8 * ac) * 2);
-    const int gt = tid & 255;                     // decode: group of this thread
-    const bool hi_half = w >= 4;                  // column half of the group (wave-uniform)
-    const int t_idx = gt >> 3, g = gt & 7;
+    for (int jj = 0; jj < 4; ++jj)
+        a_voff[jj] = (int)((min(ar0 + 64 * jj, ft.rows_valid - 1) * p.lda + 8 * ac) * 2);
+    const int t_idx = pt >> 3, g = pt & 7;  // decode: group g of tile t_idx
     const int tr = t_idx >> 4, tc = t_idx & 15;
     const int tcols = min(16, tiles_n - ft.nt * 16);
     const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
@@ -668,12 +671,12 @@ __device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, 
     }
     const int col0 = tc * 16 + g;
 
-    v4u ga[2][2];
+    v4u ga[2][4];
     uint32_t gw[2][K + 1];
     auto load = [&](int t, int r) {
         const int so = min(t, nsteps - 1);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+        for (int jj = 0; jj < 4; ++jj)
             ga[r][jj] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff[jj], so * (kTK * 2), 0));
 #pragma unroll
         for (int j = 0; j < K + 1; ++j)
@@ -683,75 +686,90 @@ __device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, 
         uint8_t* A = lds + st * kABytes;
         uint8_t* B = lds + kStages * kABytes + st * kBBytes;
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 128 * jj, ac)) = ga[r][jj];
-        if (hi_half)
-            decode_group_half<K, CB, 1>(gw[r], B, col0, 2 * tr);
-        else
-            decode_group_half<K, CB, 0>(gw[r], B, col0, 2 * tr);
+        for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[r][jj];
+        decode_group_half<K, CB, 0>(gw[r], B, col0, 2 * tr);
+        decode_group_half<K, CB, 1>(gw[r], B, col0, 2 * tr);
     };
-
-    constexpr int MFA = MF > 0 ? MF : 1;
-    float4_t acc[MFA][4];
-#pragma unroll
-    for (int i = 0; i < MFA; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-    half8_t fa[MFA], fb[4];
-    const int off_ev = swz(lane & 15, lane >> 4), off_od = swz(16 + (lane & 15), lane >> 4) - 16 * 64;
-    auto read = [&](int st) {
-        const uint8_t* A = lds + st * kABytes;
-        const uint8_t* B = lds + kStages * kABytes + st * kBBytes;
-#pragma unroll
-        for (int nf = 0; nf < 4; ++nf) {
-            const int f = 4 * wn + nf;
-            fb[nf] = *reinterpret_cast<const half8_t*>(B + f * 1024 + ((f & 1) ? off_od : off_ev));
-        }
-#pragma unroll
-        for (int i = 0; i < MF; ++i) {
-            const int f = wm + 2 * i;
-            fa[i] = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
-        }
-    };
-    auto mma = [&]() {
-#pragma unroll
-        for (int i = 0; i < MF; ++i)
-#pragma unroll
-            for (int nf = 0; nf < 4; ++nf)
-                acc[i][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[nf], acc[i][nf], 0, 0, 0);
-    };
-
-    // ---- prologue: stages 0, 1 hold steps 0, 1; register sets hold steps 2, 3
+    // prologue: stages 0, 1 hold steps 0, 1; the registers hold steps 2, 3,
+    // issued in the loop's order (register set 0 before set 1) so that the
+    // loop's first wait is for set 0 only
     load(0, 0);
     load(1, 1);
     stage(0, 0);
     stage(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
     load(2, 0);
+    __builtin_amdgcn_sched_barrier(0);
     load(3, 1);
     lds_barrier();
-
-    // ---- main loop, two k-steps per trip (nsteps is a multiple of 4)
     int st_cur = 0;  // stage of step t
     for (int t = 0; t < nsteps; t += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int st_next2 = st_cur == 0 ? 2 : st_cur - 1;  // (t + u + 2) % 3
-            if constexpr (MF > 0) read(st_cur);
-            stage(st_next2, u);
+            stage(st_cur == 0 ? 2 : st_cur - 1, u);  // step t + u + 2 into stage (t + u + 2) % 3
             load(t + u + 4, u);
-            if constexpr (MF > 0) mma();
             lds_barrier();
             st_cur = st_cur == 2 ? 0 : st_cur + 1;
         }
     }
+}
 
-    // ---- epilogue: Z * out_scale for the valid rows
-    if constexpr (MF > 0) {
-        const int colw = ft.nt * kTN + 64 * wn + (lane & 15);
+// Consumer waves (4..11): wave c = w - 4 owns row half c / 4 (row fragments
+// 8 (c / 4) + i, i < MF, of which the first my_nfr hold rows) and the 64
+// columns 64 (c % 4) of the tile; per k-step it reads its fragments from the
+// stage the producers finished one barrier earlier and issues 4 MFMAs per row
+// fragment.
+template <int MF>
+__device__ __forceinline__ void fat_consumer(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps) {
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int c = w / 3 * 2 + w % 3 - 1;  // 0..7
+    const int h = (c >> 2) & 1, cn = c & 3;
+    const int my_nfr = min(8, max(0, ((ft.rows_valid + 15) >> 4) - 8 * h));
+    const bool mma_on = my_nfr > 0 && 64 * cn < p.N - ft.nt * kTN;  // a last tile may be narrower
+    float4_t acc[MF][4];
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int off_ev = swz(lane & 15, lane >> 4), off_od = swz(16 + (lane & 15), lane >> 4) - 16 * 64;
+    auto consume = [&](int st) {
+        const uint8_t* A = lds + st * kABytes;
+        const uint8_t* B = lds + kStages * kABytes + st * kBBytes;
+        half8_t fb[4];
+#pragma unroll
+        for (int nf = 0; nf < 4; ++nf) {
+            const int f = 4 * cn + nf;
+            fb[nf] = *reinterpret_cast<const half8_t*>(B + f * 1024 + ((f & 1) ? off_od : off_ev));
+        }
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+            if (MF > 1 && i >= my_nfr) break;  // wave-uniform
+            const int f = 8 * h + i;
+            const half8_t fa = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
+#pragma unroll
+            for (int nf = 0; nf < 4; ++nf)
+                acc[i][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, fb[nf], acc[i][nf], 0, 0, 0);
+        }
+    };
+    lds_barrier();  // the producers' prologue
+    int st_cur = 0;
+    for (int t = 0; t < nsteps; t += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (mma_on) consume(st_cur);
+            lds_barrier();
+            st_cur = st_cur == 2 ? 0 : st_cur + 1;
+        }
+    }
+    // epilogue: Z * out_scale for the valid rows
+    if (mma_on) {
+        const int colw = ft.nt * kTN + 64 * cn + (lane & 15);
 #pragma unroll
         for (int i = 0; i < MF; ++i) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int r = 16 * (wm + 2 * i) + 4 * (lane >> 4) + e;
+                const int r = 16 * (8 * h + i) + 4 * (lane >> 4) + e;
                 if (r < ft.rows_valid) {
                     const int64_t o = (ft.out_row0 + r) * p.ldo + colw;
 #pragma unroll
@@ -768,22 +786,25 @@ __device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, 
     }
 }
 
+template <int CB, int K, int MF>
+__device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, uint8_t* lds) {
+    const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
+    if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) % 3 == 0)
+        fat_producer<CB, K>(p, ft, lds, nsteps);
+    else
+        fat_consumer<MF>(p, ft, lds, nsteps);
+}
+
 template <int CB, int K>
 __device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft, uint8_t* lds) {
-    // row fragments of this wave holding valid rows (row half wm takes
-    // fragments wm, wm + 2, ...), rounded up to 0, 1, 2, 4 or 8
-    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int wm = w & 1, wn = w >> 1;
-    const int nfr = (ft.rows_valid + 15) >> 4;
-    const bool cols_ok = wn * 64 < p.N - ft.nt * kTN;  // a last tile may hold 128 columns
-    const int mine = (nfr > wm && cols_ok) ? (nfr - wm + 1) >> 1 : 0;
-    if (mine == 0)
-        fat_tile<CB, K, 0>(p, ft, lds);
-    else if (mine == 1)
+    // 16-row fragments per consumer (at most 8 in either row half), rounded
+    // up to 1, 2, 4 or 8
+    const int nfr = min(8, (ft.rows_valid + 15) >> 4);
+    if (nfr <= 1)
         fat_tile<CB, K, 1>(p, ft, lds);
-    else if (mine == 2)
+    else if (nfr <= 2)
         fat_tile<CB, K, 2>(p, ft, lds);
-    else if (mine <= 4)
+    else if (nfr <= 4)
         fat_tile<CB, K, 4>(p, ft, lds);
     else
         fat_tile<CB, K, 8>(p, ft, lds);
@@ -796,7 +817,7 @@ __device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft
 // (csrc/p2b_moe.cu:295-324).  Two kernels, so that the K 5/6 decode's
 // registers never weigh on the common kernel's allocation.
 template <int CB, int KSET>
-__global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fat_gemm_kernel(
+__global__ __launch_bounds__(kFatThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void fat_gemm_kernel(
     FatParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     FatTile ft;
