@@ -714,19 +714,17 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
     }
 }
 
-// Consumer waves (4..11): wave c = w - 4 owns row half c / 4 (row fragments
-// 8 (c / 4) + i, i < MF, of which the first my_nfr hold rows) and the 64
-// columns 64 (c % 4) of the tile; per k-step it reads its fragments from the
-// stage the producers finished one barrier earlier and issues 4 MFMAs per row
-// fragment.
+// Consumer waves (eight): wave c owns row half h = c / 4 (row fragments
+// 8 h + i, i < MF: the fragments of its half that hold rows, rounded up) and
+// the 64 columns 64 (c % 4) of the tile; per k-step it reads its fragments
+// from the stage the producers finished one barrier earlier and issues 4
+// MFMAs per row fragment.  No branch sits between the reads and the MFMAs,
+// so that all of a step's reads are in flight before the first MFMA waits.
 template <int MF>
-__device__ __forceinline__ void fat_consumer(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps) {
+__device__ __forceinline__ void fat_consumer(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps,
+                                             int c, bool mma_on) {
     const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int c = w / 3 * 2 + w % 3 - 1;  // 0..7
     const int h = (c >> 2) & 1, cn = c & 3;
-    const int my_nfr = min(8, max(0, ((ft.rows_valid + 15) >> 4) - 8 * h));
-    const bool mma_on = my_nfr > 0 && 64 * cn < p.N - ft.nt * kTN;  // a last tile may be narrower
     float4_t acc[MF][4];
 #pragma unroll
     for (int i = 0; i < MF; ++i)
@@ -744,7 +742,6 @@ __device__ __forceinline__ void fat_consumer(const FatParams& p, const FatTile& 
         }
 #pragma unroll
         for (int i = 0; i < MF; ++i) {
-            if (MF > 1 && i >= my_nfr) break;  // wave-uniform
             const int f = 8 * h + i;
             const half8_t fa = *reinterpret_cast<const half8_t*>(A + f * 1024 + ((f & 1) ? off_od : off_ev));
 #pragma unroll
@@ -786,28 +783,29 @@ __device__ __forceinline__ void fat_consumer(const FatParams& p, const FatTile& 
     }
 }
 
-template <int CB, int K, int MF>
-__device__ __forceinline__ void fat_tile(const FatParams& p, const FatTile& ft, uint8_t* lds) {
-    const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
-    if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) % 3 == 0)
-        fat_producer<CB, K>(p, ft, lds, nsteps);
-    else
-        fat_consumer<MF>(p, ft, lds, nsteps);
-}
-
 template <int CB, int K>
 __device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft, uint8_t* lds) {
-    // 16-row fragments per consumer (at most 8 in either row half), rounded
-    // up to 1, 2, 4 or 8
-    const int nfr = min(8, (ft.rows_valid + 15) >> 4);
+    const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (w % 3 == 0) {  // waves 0, 3, 6, 9: one per SIMD however the waves are placed
+        fat_producer<CB, K>(p, ft, lds, nsteps);
+        return;
+    }
+    // consumers: the wave's 16-row fragments holding rows (at most 8 in its
+    // row half), rounded up to 1, 2, 4, 6 or 8 (wave-uniform)
+    const int c = w / 3 * 2 + w % 3 - 1;  // 0..7
+    const int nfr = min(8, max(0, ((ft.rows_valid + 15) >> 4) - 8 * ((c >> 2) & 1)));
+    const bool mma_on = nfr > 0 && 64 * (c & 3) < p.N - ft.nt * kTN;  // a last tile may be narrower
     if (nfr <= 1)
-        fat_tile<CB, K, 1>(p, ft, lds);
+        fat_consumer<1>(p, ft, lds, nsteps, c, mma_on);
     else if (nfr <= 2)
-        fat_tile<CB, K, 2>(p, ft, lds);
+        fat_consumer<2>(p, ft, lds, nsteps, c, mma_on);
     else if (nfr <= 4)
-        fat_tile<CB, K, 4>(p, ft, lds);
+        fat_consumer<4>(p, ft, lds, nsteps, c, mma_on);
+    else if (nfr <= 6)
+        fat_consumer<6>(p, ft, lds, nsteps, c, mma_on);
     else
-        fat_tile<CB, K, 8>(p, ft, lds);
+        fat_consumer<8>(p, ft, lds, nsteps, c, mma_on);
 }
 
 // KSET 0: tiles of K 2..4 (every uniform-K launch and most of a mixed-K
