@@ -6,25 +6,26 @@
 // src/vllm_exl3/exl3.py:2981-3599, which sort on the host and loop over fat
 // experts in Python).
 //
-// GEMM tile: one 512-thread workgroup (8 wave64s in a 2x4 grid, two per
-// SIMD) owns 256 rows x 256 output columns of one expert; each wave
-// accumulates 128x64 with v_mfma_f32_16x16x32_f16.  Per 32-deep k-step, the
-// packed trellis of the step (2 tile rows x 16 tiles) is decoded ONCE by the
-// workgroup into an LDS B tile of real fp16 weights (the codebook's two
-// halves summed with one packed fp16 add, which rounds the exact sum once
-// like the reference's decoder) and reused by every row of the tile.  Two
-// threads share the 32 weights of one 8-index group of one tile, one column
-// half each: for such a group the window offsets inside the group's K+1
+// GEMM tile: one 768-thread workgroup (12 wave64s, three per SIMD) owns 256
+// rows x 256 output columns of one expert.  Four producer waves (one per
+// SIMD) load, stage and decode; eight MFMA waves (2 row halves x 4 column
+// quarters) accumulate 128x64 each with v_mfma_f32_16x16x32_f16, so a
+// SIMD's VALU decodes the next stage while its matrix core runs the current
+// one.  Per 32-deep k-step, the packed trellis of the step (2 tile rows x 16
+// tiles) is decoded ONCE into an LDS B tile of real fp16 weights (the
+// codebook's two halves summed with one packed fp16 add, which rounds the
+// exact sum once like the reference's decoder) and reused by every row of
+// the tile.  A producer thread decodes one 8-index group of one tile (32
+// weights, both column halves): the window offsets inside the group's K+1
 // words are compile-time constants, so the decode needs no dynamic register
 // indexing; each 16-byte unit produced is eight consecutive k of one column,
 // exactly one MFMA B-operand lane fragment, stored with one ds_write_b128.
 //
-// Pipeline (one barrier per k-step, three LDS stages): global loads of A rows
-// and packed bits run two k-steps ahead of their staging; iteration t reads
-// the operands of step t, decodes and stages step t + 2 and issues the MFMAs
-// of step t, and the other wave on the SIMD fills the MFMA and LDS latencies.
-// Waves whose 128-row slice holds no rows of the expert skip their MFMAs but
-// still share the decode.
+// Pipeline (one barrier per k-step, three LDS stages): the producers' global
+// loads of A rows and packed bits run two k-steps ahead of their staging;
+// iteration t: the MFMA waves read and multiply step t while the producers
+// decode and stage step t + 2 and issue the loads of step t + 4.  An MFMA
+// wave covers only the row fragments of its half that hold rows.
 //
 // The output rotation is not done in the GEMM epilogue: the GEMM stores
 // Z / sqrt(128) (Z = A x Wq) and the consumer kernel - the activation kernel,
@@ -607,19 +608,12 @@ __global__ __launch_bounds__(256) void linear_out_kernel(const float* z, int N, 
 }
 
 // ---------------------------------------------------------------------------
-// The GEMM tile: 256 x 256 outputs computed by 8 waves (2 row halves x 4
-// column quarters, 128 x 64 each, 128 accumulator registers), two waves per
-// SIMD, so that the decode VALU of one runs beside the other's MFMAs (a
-// wave's own MFMAs and VALU do not overlap; with one 128 x 128 wave per SIMD
-// they ran back to back).  Operands are read from LDS just before their MFMAs
-// (single-buffered: the other wave covers the latency), so three LDS stages
-// keep one barrier per k-step: step t lives in stage t % 3; iteration t reads
-// step t, stages step t + 2 (into the stage step t - 1 used, whose reads all
-// waves finished before the previous barrier), issues the global loads of
-// step t + 4 and runs the MFMAs of step t.  Staging: two 16-byte A chunks
-// per thread; each trellis group is decoded by two threads, one per column
-// half (waves 0-3 take half 0, waves 4-7 half 1, so the choice is uniform
-// per wave).
+// The GEMM tile (see the top of this file): 256 x 256 outputs, four producer
+// waves and eight MFMA waves (128 x 64 outputs, 128 accumulator registers
+// each); three LDS stages keep one barrier per k-step: step t lives in stage
+// t % 3; iteration t multiplies step t, stages step t + 2 (into the stage step
+// t - 1 used, whose reads all waves finished before the previous barrier) and
+// loads step t + 4.
 constexpr int kFatThreads = 768;
 constexpr int kFatProducers = 4;  // waves that load, decode and stage; the other eight run the MFMAs
 constexpr int kStages = 3;
