@@ -39,8 +39,10 @@ ORACLE_PINS = {
     "read_window": "every bit position of K=2,3,4,8 tiles vs oracle/_ref; brute-force bit list",
     "tile_position": "bijection + literal swizzle loop of csrc/bindings.cpp:51-75",
     "hadamard": "vs oracle/_ref (bit-exact); H.H = 128 I; float64 matrix form",
-    "dequant": "composition: float64 diag(suh) H Wq H diag(svh)/128 within one fp16 ulp; "
-               "suh=svh=1 round trip; constant tile gives one non-zero per block",
+    "dequant": "bit-exact vs the reference's own dequant_cpu (csrc/bindings.cpp:15-100, compiled in "
+               "place by oracle/ref_dequant_harness.cpp) for K 1..4, 8, MCG and mul1; float64 "
+               "diag(suh) H Wq H diag(svh)/128 within one fp16 ulp; suh=svh=1 round trip; constant "
+               "tile gives one non-zero per block",
     "moe_loop": "tests/test_oracle_moe.py: the reference's activation vectors "
                 "(tests/test_activation_parity.py:46-81: 400.0, 99.9954605, five clamp "
                 "boundaries, non-positive limits); SwiGLU-OAI and relu2 closed forms; a "

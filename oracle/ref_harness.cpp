@@ -7,9 +7,8 @@
 //   hadamard              csrc/exl3_dequant.cuh:168-179
 //   float_to_half_bits    csrc/exl3_dequant.cuh:40-86
 //   half_bits_to_float    csrc/exl3_dequant.cuh:25-38
-// The full dequant_cpu (csrc/bindings.cpp:15-100) sits in a torch/pybind
-// translation unit that also references CUDA-only symbols, so it is not
-// buildable here; the oracle's composition is pinned by other checks.
+// The full dequant_cpu (csrc/bindings.cpp:15-100) is built separately by
+// ref_dequant_harness.cpp (its translation unit needs the torch headers).
 #include <cstddef>
 #include <cstdint>
 #include "exl3_dequant.cuh"

@@ -2,8 +2,9 @@
 
 Pins: the reference's own golden vectors (tests/test_dequant_parity.py of the
 reference), the reference's compiled primitives (oracle/_ref, built from
-csrc/exl3_dequant.cuh where it lies), numpy's IEEE casts, and closed forms of
-the Hadamard composition.
+csrc/exl3_dequant.cuh where it lies) and its whole dequant_cpu
+(csrc/bindings.cpp:15-100, compiled in place by oracle/ref_dequant_harness.cpp),
+numpy's IEEE casts, and closed forms of the Hadamard composition.
 """
 
 import ctypes
@@ -144,6 +145,62 @@ def test_hadamard_vs_reference_and_closed_form(ref):
         np.testing.assert_allclose(a, O.hadamard_matrix(128) @ v.astype(np.float64), rtol=1e-5, atol=1e-4)
     h = O.hadamard_matrix(128)
     assert np.array_equal(h @ h, 128 * np.eye(128))
+
+
+REF_DEQUANT_SO = ROOT / "oracle" / "_ref" / "libref_dequant.so"
+
+
+@pytest.fixture(scope="module")
+def ref_dequant():
+    """The reference's own dequant_cpu (csrc/bindings.cpp:15-100), compiled in
+    place by oracle/Makefile (oracle/ref_dequant_harness.cpp)."""
+    if not REF_DEQUANT_SO.exists():
+        pytest.skip("oracle/_ref/libref_dequant.so not built (reference checkout absent)")
+    import os
+
+    import torch  # noqa: F401  (the harness links libtorch)
+
+    lib = ctypes.CDLL(str(REF_DEQUANT_SO), mode=os.RTLD_LAZY)
+    fn = lib.ref_dequant_cpu
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    return fn
+
+
+@pytest.mark.parametrize("K,cb", [(2, 1), (3, 2), (4, 1), (4, 2), (8, 1), (1, 2)])
+def test_dequant_bit_exact_vs_reference_dequant_cpu(ref_dequant, K, cb):
+    """The whole composition (window read, codebook, swizzle, both Hadamard
+    passes, suh/svh, fp16 rounding) against the reference's own dequant_cpu:
+    bit for bit (MCG and mul1, the codebooks its mcg flag reaches)."""
+    g = np.random.default_rng(200 + K * 3 + cb)
+    tk, tn = 16, 24  # 256 x 384
+    t = g.integers(0, 65536, size=(tk, tn, 16 * K), dtype=np.uint16).view(np.int16)
+    su = np.where(g.random(tk * 16) < 0.5, -1.0, 1.0).astype(np.float16)
+    sv = (np.where(g.random(tn * 16) < 0.5, -1.0, 1.0) * g.uniform(0.005, 0.02, tn * 16)).astype(np.float16)
+    out = np.zeros((tk * 16, tn * 16), np.uint16)
+    assert ref_dequant(t.ctypes.data, tk, tn, su.ctypes.data, sv.ctypes.data, K, 1 if cb == 1 else 0,
+                       out.ctypes.data) == 0
+    w = O.dequant(t, su, sv, K, cb)
+    assert np.array_equal(out, np.asarray(w, np.float16).view(np.uint16))
+
+
+def test_reference_dequant_catches_a_reordered_composition(ref_dequant):
+    """A plausible mistake -- the scales applied before the second Hadamard
+    pass instead of after -- stays within an ulp of the float64 form but is
+    not bit-identical to the reference."""
+    g = np.random.default_rng(9)
+    t = g.integers(0, 65536, size=(8, 8, 64), dtype=np.uint16).view(np.int16)
+    su = (np.where(g.random(128) < 0.5, -1.0, 1.0) * g.uniform(0.5, 2.0, 128)).astype(np.float16)
+    sv = (np.where(g.random(128) < 0.5, -1.0, 1.0) * g.uniform(0.005, 0.02, 128)).astype(np.float16)
+    out = np.zeros((128, 128), np.uint16)
+    ref_dequant(t.ctypes.data, 8, 8, su.ctypes.data, sv.ctypes.data, 4, 1, out.ctypes.data)
+    q = O.decode_tiles(t, 4, 1).astype(np.float32)
+    norm = np.float32(0.088388347648)
+    a = O.block_hadamard(q * su.astype(np.float32)[:, None], axis=1).astype(np.float32) * norm
+    wrong = (O.block_hadamard(a, axis=0).astype(np.float32) * norm * sv.astype(np.float32)[None, :])
+    assert not np.array_equal(out, wrong.astype(np.float16).view(np.uint16))
+    assert np.array_equal(out, np.asarray(O.dequant(t, su, sv, 4, 1), np.float16).view(np.uint16))
 
 
 @pytest.mark.parametrize("K,cb", [(2, 1), (3, 0), (4, 1), (4, 2), (8, 1)])
