@@ -563,6 +563,48 @@ def q4_stage_prefill(S, torch, dev, steps, warmup, PhaseTimer):
             "per_prefix": out}
 
 
+def q4_sparse_decode_leg(S, torch, dev, steps, warmup, PhaseTimer):
+    """NVFP4 block-sparse decode attention (q4_sparse_decode): 64 decode
+    sequences, 24 query / 4 KV heads (one rank of a 48 / 8-head model at
+    tensor parallel 2), 16 selected 128-token blocks per query token and KV
+    head out of a 16,384-token context, pages in random pool order."""
+    from vllm_exl3_amd import nvfp4_kv as Q
+
+    B, Hq, Hkv, L, topk = 64, 24, 4, 16384, 16
+    n_blocks = L // 128
+    k, v = S.kv_inputs_device(9, B, Hkv, L, dev)
+    bt = torch.from_numpy(S.block_table(9, B, n_blocks)).to(dev)
+    sl = torch.full((B,), L, dtype=torch.int32, device=dev)
+    pool = Q.new_pool(B * n_blocks, Hkv, dev)
+    Q.pack_pages(k, v, sl, bt, pool)
+    del k, v
+    g = torch.Generator().manual_seed(10)
+    tk = torch.stack([torch.stack([torch.randperm(n_blocks, generator=g)[:topk] for _ in range(B)])
+                      for _ in range(Hkv)]).to(torch.int32).to(dev)  # [Hkv, B, topk]
+    q = torch.from_numpy(S.activations(11, B * Hq, 128).reshape(B, Hq, 128)).to(dev).bfloat16()
+    out = torch.empty_like(q)
+    scale = 1.0 / 128 ** 0.5
+    call = lambda: Q.q4_sparse_decode(q, pool, tk, bt, sl, Hkv, scale, out, 1)  # noqa: E731
+    ev = event_stats(torch, call, steps, warmup)
+    _, pt = time_steps(torch, call, steps, 1, PhaseTimer)
+    kv_bytes = B * Hkv * topk * 2 * 9216  # K and V slot regions of every selected block
+    nbytes = kv_bytes + 2 * q.numel() * 2
+    att_us = pt.mean_ms(0) * 1e3
+    del pool
+    return {
+        "workload": f"NVFP4 q4 sparse decode, B{B} Hq{Hq} Hkv{Hkv} d128, top-{topk} of {n_blocks} 128-token "
+                    f"blocks per query and KV head",
+        "us_per_step": round(ev["mean_ms"] * 1e3, 2),
+        "median_us": round(ev["median_ms"] * 1e3, 2), "p95_us": round(ev["p95_ms"] * 1e3, 2),
+        "bytes_per_step": nbytes,
+        "gbs": round(nbytes / (ev["median_ms"] * 1e-3) / 1e9, 1),
+        "decode_kernel_us": round(att_us, 2),
+        "decode_kernel_gbs": round(kv_bytes / (att_us * 1e-6) / 1e9, 1),
+        "frac_hbm_peak": round(kv_bytes / (att_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "merge_us": round(pt.mean_ms(1) * 1e3, 2),
+    }
+
+
 def crossover(args) -> int:
     """Median µs per call of moe_forward (decode executor) and moe_prefill
     (prefill executor) for T tokens, softmax top-8 routing, on two layer
@@ -643,7 +685,7 @@ def main() -> int:
                     help="distinct C1 layers the decode steps rotate over (HBM-resident weights)")
     ap.add_argument("--configs", default="c0,c2,c3,c4,q4",
                     help="other BASELINE configs reported beside the headline (c0,c2,c3,c4 and q4, the "
-                         "q4 prefill staging; '' = none)")
+                         "q4 prefill staging and sparse decode; '' = none)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
@@ -782,6 +824,7 @@ def main() -> int:
         line["kv_decode_c4"] = kv_decode_c4(S, torch, dev, args.steps, args.warmup, PhaseTimer)
     if "q4" in others:
         line["q4_stage"] = q4_stage_prefill(S, torch, dev, args.steps, args.warmup, PhaseTimer)
+        line["q4_sparse_decode"] = q4_sparse_decode_leg(S, torch, dev, args.steps, args.warmup, PhaseTimer)
     if not args.no_cpu_baseline:
         import oracle as O
 

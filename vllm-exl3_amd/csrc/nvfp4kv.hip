@@ -37,7 +37,6 @@ constexpr int kQ4Slot = 9216;
 constexpr int kQ4Data = 8192;
 constexpr int kQ4MaxGroup = 16;   // query heads per KV head
 constexpr int kQ4Threads = 256;
-constexpr int kQ4Pitch = kQ4Dim + 8;  // fp16 LDS row pitch (bank spread)
 
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -399,52 +398,101 @@ struct Q4DecodeParams {
     float* lse_part;           // [chunks][total_q][Hq]
 };
 
-// Dequantise one 9216-byte slot into LDS as fp16 [128][kQ4Pitch]; thread
-// tid handles token tid/2, dims [64 (tid & 1), +64).
-__device__ __forceinline__ void stage_slot(const uint8_t* region, int side, uint16_t* lds, int tid) {
-    const int t = tid >> 1, half = tid & 1;
-    const u32x4* src = reinterpret_cast<const u32x4*>(region + t * 64 + 32 * half);
-    const u32x4 d0 = src[0], d1 = src[1];
-    uint32_t w[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-    uint32_t* dst = reinterpret_cast<uint32_t*>(lds + t * kQ4Pitch + 64 * half);
+// ---------------------------------------------------------------------------
+// Block-sparse decode on the matrix cores.  Workgroup = (query token, KV head,
+// chunk of the top-k list), four waves.  Per listed block (128 tokens):
+//   * staging: every thread converts 64 K and 64 V values of one token with
+//     v_cvt_scalef32_pk_f16_fp4 and one packed multiply per pair (e2m1 x its
+//     group's e4m3 scale, exact in fp16) into LDS: K as [token][dim], V
+//     transposed as [dim][token]; the packed bytes are loaded one block
+//     ahead;
+//   * scores S[head][token] = q . k on v_mfma_f32_16x16x32_f16 (A = the G
+//     query heads of the KV head, padded to 16 rows, fp16 from registers;
+//     B = K), wave w takes tokens 32w..32w+31; scaled to the log2 domain in
+//     fp32, tokens past the query's position masked;
+//   * online softmax in fp32: block maxima across the waves through LDS,
+//     P = 2^(S - m) rounded to fp16 into LDS as [head][token];
+//   * O[head][dim] += P V on the same MFMA (A = P, B = V), wave w takes dims
+//     32w..32w+31; O and each wave's share of the denominator are rescaled
+//     by 2^(m_old - m_new).
+// The chunk's normalised output and its log2-sum-exp go to the workspace.
+// ---------------------------------------------------------------------------
+constexpr int kQ4Pitch = kQ4Dim + 8;  // fp16 LDS row pitch: 272 bytes, 16-byte aligned, banks spread
+
+struct Q4Lds {
+    uint16_t K[kQ4Page * kQ4Pitch];      // [token][dim]
+    uint16_t Vt[kQ4Dim * kQ4Pitch];      // [dim][token]
+    uint16_t P[kQ4MaxGroup * kQ4Pitch];  // [head][token]
+    float red[4][kQ4MaxGroup];           // per-wave block maxima
+    float lsum[4][kQ4MaxGroup];          // per-wave denominators
+};
+
+// The packed bytes one thread stages: token t = tid / 2, dims 64 h .. 64 h + 63
+// (h = tid & 1) of the K and of the V slot, and the four group scales of each.
+struct Q4Piece {
+    u32x4 k0, k1, v0, v1;
+    uint32_t ks, vs;  // scale bytes of groups 4h .. 4h + 3, one per byte
+};
+
+__device__ __forceinline__ void q4_load_piece(const uint8_t* base, int tid, Q4Piece& pc) {
+    const int t = tid >> 1, h = tid & 1;
+    const u32x4* ksrc = reinterpret_cast<const u32x4*>(base + t * 64 + 32 * h);
+    const u32x4* vsrc = reinterpret_cast<const u32x4*>(base + kQ4Slot + t * 64 + 32 * h);
+    pc.k0 = ksrc[0];
+    pc.k1 = ksrc[1];
+    pc.v0 = vsrc[0];
+    pc.v1 = vsrc[1];
+    uint32_t ks = 0, vs = 0;
 #pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {  // groups 4 half + gi (16 dims = 2 words)
-        const float sc = e4m3_value(region[kQ4Data + scale_offset(side, t, 4 * half + gi)]);
-        const h2v s2 = {(_Float16)sc, (_Float16)sc};
+    for (int gi = 0; gi < 4; ++gi) {
+        ks |= (uint32_t)base[kQ4Data + scale_offset(0, t, 4 * h + gi)] << (8 * gi);
+        vs |= (uint32_t)base[kQ4Slot + kQ4Data + scale_offset(1, t, 4 * h + gi)] << (8 * gi);
+    }
+    pc.ks = ks;
+    pc.vs = vs;
+}
+
+// The eight fp16 values of one packed word (dims 2b, 2b + 1 in byte b, low
+// nibble first), each e2m1 code times the group scale sc.  The conversion's
+// own scale operand acts as a power of two (the exponent of an MX block
+// scale), so the e4m3 scale is applied by one packed fp16 multiply per pair,
+// which is exact: an e2m1 x e4m3 product has at most 7 significant bits.
+__device__ __forceinline__ u32x4 q4_cvt_word(uint32_t w, float sc) {
+    const h2v s2 = {(_Float16)sc, (_Float16)sc};
+    const h2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * s2;
+    const h2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * s2;
+    const h2v c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * s2;
+    const h2v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * s2;
+    return u32x4{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, c),
+                 __builtin_bit_cast(uint32_t, d)};
+}
+
+__device__ __forceinline__ void q4_stage_piece(const Q4Piece& pc, int tid, Q4Lds& L) {
+    const int t = tid >> 1, h = tid & 1;
+    const uint32_t kw[8] = {pc.k0.x, pc.k0.y, pc.k0.z, pc.k0.w, pc.k1.x, pc.k1.y, pc.k1.z, pc.k1.w};
+    const uint32_t vw[8] = {pc.v0.x, pc.v0.y, pc.v0.z, pc.v0.w, pc.v1.x, pc.v1.y, pc.v1.z, pc.v1.w};
+    u32x4* krow = reinterpret_cast<u32x4*>(L.K + t * kQ4Pitch + 64 * h);
 #pragma unroll
-        for (int wi = 0; wi < 2; ++wi) {
-            const uint32_t word = w[2 * gi + wi];
+    for (int j = 0; j < 8; ++j) {  // word j: dims 64 h + 8 j .. + 7, group 4 h + j / 2
+        const float ksc = e4m3_value((pc.ks >> (8 * (j >> 1))) & 0xFFu);
+        krow[j] = q4_cvt_word(kw[j], ksc);
+        const float vsc = e4m3_value((pc.vs >> (8 * (j >> 1))) & 0xFFu);
+        const u32x4 v = q4_cvt_word(vw[j], vsc);
+        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int by = 0; by < 4; ++by) {
-                h2v v = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word >> (8 * by), 1.0f, 0);
-                v = v * s2;  // exact: e2m1 x e4m3 fits fp16
-                dst[(2 * gi + wi) * 4 + by] = __builtin_bit_cast(uint32_t, v);
-            }
+        for (int e = 0; e < 8; ++e) {
+            const int d = 64 * h + 8 * j + e;
+            L.Vt[d * kQ4Pitch + t] = (uint16_t)(vv[e >> 1] >> (16 * (e & 1)));
         }
     }
 }
 
-struct Q4Lds {
-    uint16_t K[kQ4Page * kQ4Pitch];
-    uint16_t V[kQ4Page * kQ4Pitch];
-    float q[kQ4MaxGroup][kQ4Dim];
-    float p[kQ4MaxGroup][kQ4Page];
-    float red[kQ4MaxGroup][4];
-    float m[kQ4MaxGroup], l[kQ4MaxGroup], alpha[kQ4MaxGroup];
-};
-
 __global__ __launch_bounds__(kQ4Threads) void q4_decode_kernel(Q4DecodeParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
     Q4Lds& L = *reinterpret_cast<Q4Lds*>(q4_lds);
-    uint16_t* Ks = L.K;
-    uint16_t* Vs = L.V;
-    float (*qs)[kQ4Dim] = L.q;
-    float (*ps)[kQ4Page] = L.p;
-    float (*red)[4] = L.red;
-    float* m_s = L.m;
-    float* l_s = L.l;
-    float* alpha_s = L.alpha;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
     const int i = blockIdx.x % p.total_q;
     const int c = blockIdx.x / p.total_q;
     const int h = blockIdx.y;
@@ -456,115 +504,152 @@ __global__ __launch_bounds__(kQ4Threads) void q4_decode_kernel(Q4DecodeParams p)
     const int real_topk = min(p.max_topk, n_blocks);
     const int chunk = (p.max_topk + p.n_chunks - 1) / p.n_chunks;
     const int c0 = c * chunk, c1 = min(c0 + chunk, real_topk);
-
-    for (int e = tid; e < G * kQ4Dim; e += kQ4Threads) {
-        const int hh = e / kQ4Dim, d = e % kQ4Dim;
-        qs[hh][d] = q4_load(p.q, p.q_dtype, (int64_t)i * p.q_sn + (int64_t)(h * G + hh) * p.q_sh + d) *
-                    p.scale_log2;
-    }
-    if (tid < kQ4MaxGroup) {
-        m_s[tid] = -INFINITY;
-        l_s[tid] = 0.0f;
-    }
-    // thread tid accumulates O[hh][d] for d = tid % 128, heads tid/128, +2, ...
-    const int od = tid & 127, oh0 = tid >> 7;
-    float acc[kQ4MaxGroup / 2];
-#pragma unroll
-    for (int k = 0; k < kQ4MaxGroup / 2; ++k) acc[k] = 0.0f;
     const int* tk = p.topk + (int64_t)h * p.tk_sh + (int64_t)i * p.tk_sn;
     const int* bt = p.block_table + (int64_t)req * p.bt_stride;
 
-    for (int e = c0; e < c1; ++e) {
-        const int blk = tk[e];
-        if (blk < 0 || blk >= n_blocks) continue;  // uniform
-        const int64_t page = bt[blk];
-        if (page < 0 || page >= p.num_pages) continue;
-        const uint8_t* base = p.pool + (page * (2 * p.Hkv) + 2 * h) * (int64_t)kQ4Slot;
-        __syncthreads();  // previous block's LDS reads are done
-        stage_slot(base, 0, Ks, tid);
-        stage_slot(base + kQ4Slot, 1, Vs, tid);
-        __syncthreads();
-        const int n_tok = min(kQ4Page, kv_len - blk * kQ4Page);
-        // scores (log2 domain): thread -> token tid % 128, heads tid/128, +2, ...
-        const int t = tid & 127;
-        float bmax[kQ4MaxGroup / 2];
+    // query fragments (A operand): head m16 (zero past G), dims 32 s + 8 g .. + 7
+    half8_t qa[4];
 #pragma unroll
-        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
-            const int hh = oh0 + 2 * k;
-            float sc = -INFINITY;
-            if (hh < G && t < n_tok) {
-                float s = 0.0f;
-                const uint32_t* kr = reinterpret_cast<const uint32_t*>(Ks + t * kQ4Pitch);
-#pragma unroll 8
-                for (int d2 = 0; d2 < kQ4Dim / 2; ++d2) {
-                    const h2v kv = __builtin_bit_cast(h2v, kr[d2]);
-                    s = __builtin_fmaf(qs[hh][2 * d2], (float)kv[0], s);
-                    s = __builtin_fmaf(qs[hh][2 * d2 + 1], (float)kv[1], s);
-                }
-                sc = s;
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = m16 < G ? q4_load(p.q, p.q_dtype, (int64_t)i * p.q_sn + (int64_t)(h * G + m16) * p.q_sh +
+                                                                  32 * s + 8 * g + e)
+                                    : 0.0f;
+            qa[s][e] = (_Float16)v;
+        }
+    }
+    float4_t o[2];  // O[heads 4 g .. 4 g + 3][dims 32 wave + 16 j + m16]
+    o[0] = float4_t{0.f, 0.f, 0.f, 0.f};
+    o[1] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run[4], l_run[4];  // per head 4 g + r: running max, this lane's share of the denominator
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m_run[r] = -INFINITY;
+        l_run[r] = 0.0f;
+    }
+
+    // the next listed block that exists (uniform)
+    auto next_valid = [&](int e, int64_t& page, int& blk) {
+        for (; e < c1; ++e) {
+            blk = tk[e];
+            if (blk < 0 || blk >= n_blocks) continue;
+            page = bt[blk];
+            if (page < 0 || page >= p.num_pages) continue;
+            return e;
+        }
+        return c1;
+    };
+    int64_t page = 0;
+    int blk = 0;
+    int e = next_valid(c0, page, blk);
+    Q4Piece pc;
+    if (e < c1) q4_load_piece(p.pool + (page * (2 * p.Hkv) + 2 * h) * (int64_t)kQ4Slot, tid, pc);
+    while (e < c1) {
+        const int cur_blk = blk;
+        __syncthreads();  // the previous block's LDS reads are done
+        q4_stage_piece(pc, tid, L);
+        int64_t npage = 0;
+        int nblk = 0;
+        const int en = next_valid(e + 1, npage, nblk);
+        if (en < c1) q4_load_piece(p.pool + (npage * (2 * p.Hkv) + 2 * h) * (int64_t)kQ4Slot, tid, pc);
+        __syncthreads();
+        const int n_tok = min(kQ4Page, kv_len - cur_blk * kQ4Page);
+
+        // scores: tokens 32 wave + 16 j + m16 (j = 0, 1), heads 4 g + r
+        float4_t sc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            sc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+            const uint16_t* krow = L.K + (32 * wave + 16 * j + m16) * kQ4Pitch + 8 * g;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const half8_t kb = *reinterpret_cast<const half8_t*>(krow + 32 * s);
+                sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, sc[j], 0, 0, 0);
             }
-            if (hh < G) ps[hh][t] = sc;
-            bmax[k] = sc;
         }
-        // block max per head: wave reduction then across the two waves of a head
+        float bmax[4];
 #pragma unroll
-        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
-            float v = bmax[k];
-            for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-            const int hh = oh0 + 2 * k;
-            if (lane == 0 && hh < G) red[hh][wave & 1] = v;
-        }
-        __syncthreads();
-        if (tid < G) {
-            const float mb = fmaxf(red[tid][0], red[tid][1]);
-            const float mn = fmaxf(m_s[tid], mb);
-            alpha_s[tid] = exp2f(m_s[tid] - mn);  // 0 when the old max is -inf
-            m_s[tid] = mn;
-        }
-        __syncthreads();
-        // probabilities and their sums
-        float bsum[kQ4MaxGroup / 2];
+        for (int r = 0; r < 4; ++r) {
+            float mx = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
-            const int hh = oh0 + 2 * k;
-            float pv = 0.0f;
-            if (hh < G) {
-                const float sc = ps[hh][t];
-                pv = sc == -INFINITY ? 0.0f : exp2f(sc - m_s[hh]);
-                ps[hh][t] = pv;
+            for (int j = 0; j < 2; ++j) {
+                const int t = 32 * wave + 16 * j + m16;
+                const float v = t < n_tok ? sc[j][r] * p.scale_log2 : -INFINITY;
+                sc[j][r] = v;
+                mx = fmaxf(mx, v);
             }
-            bsum[k] = pv;
-        }
 #pragma unroll
-        for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
-            float v = bsum[k];
-            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-            const int hh = oh0 + 2 * k;
-            if (lane == 0 && hh < G) red[hh][2 + (wave & 1)] = v;
+            for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
+            bmax[r] = mx;
+        }
+        if (m16 == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) L.red[wave][4 * g + r] = bmax[r];
         }
         __syncthreads();
-        if (tid < G) l_s[tid] = l_s[tid] * alpha_s[tid] + red[tid][2] + red[tid][3];
-        // P.V: thread -> dim od, heads oh0, +2, ...
+        float alpha[4];
 #pragma unroll
-        for (int k = 0; k < kQ4MaxGroup / 2; ++k)
-            if (oh0 + 2 * k < G) acc[k] *= alpha_s[oh0 + 2 * k];
-        for (int tt = 0; tt < n_tok; ++tt) {
-            const float vv = (float)__builtin_bit_cast(_Float16, Vs[tt * kQ4Pitch + od]);
+        for (int r = 0; r < 4; ++r) {
+            const int hh = 4 * g + r;
+            const float mb = fmaxf(fmaxf(L.red[0][hh], L.red[1][hh]), fmaxf(L.red[2][hh], L.red[3][hh]));
+            const float mn = fmaxf(m_run[r], mb);
+            alpha[r] = exp2f(m_run[r] - mn);  // 0 while the old max is -inf
+            m_run[r] = mn;
+            float ls = 0.0f;
 #pragma unroll
-            for (int k = 0; k < kQ4MaxGroup / 2; ++k)
-                if (oh0 + 2 * k < G) acc[k] = __builtin_fmaf(ps[oh0 + 2 * k][tt], vv, acc[k]);
+            for (int j = 0; j < 2; ++j) {
+                const float pv = sc[j][r] == -INFINITY ? 0.0f : exp2f(sc[j][r] - mn);
+                const _Float16 ph = (_Float16)pv;
+                ls += (float)ph;
+                L.P[hh * kQ4Pitch + 32 * wave + 16 * j + m16] = __builtin_bit_cast(uint16_t, ph);
+            }
+            l_run[r] = l_run[r] * alpha[r] + ls;
         }
+        __syncthreads();
+        // O[heads][dims 32 wave + 16 j + m16] = alpha O + P V
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[j][r] *= alpha[r];
+            const uint16_t* vrow = L.Vt + (32 * wave + 16 * j + m16) * kQ4Pitch + 8 * g;
+            const uint16_t* prow = L.P + m16 * kQ4Pitch + 8 * g;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const half8_t pa = *reinterpret_cast<const half8_t*>(prow + 32 * s);
+                const half8_t vb = *reinterpret_cast<const half8_t*>(vrow + 32 * s);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[j], 0, 0, 0);
+            }
+        }
+        e = en;
+        page = npage;
+        blk = nblk;
+    }
+    // denominators: this lane's shares over the 16 lanes of its head group,
+    // then over the four waves
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float v = l_run[r];
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
+        l_run[r] = v;
+    }
+    __syncthreads();
+    if (m16 == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) L.lsum[wave][4 * g + r] = l_run[r];
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kQ4MaxGroup / 2; ++k) {
-        const int hh = oh0 + 2 * k;
-        if (hh < G) {
-            const float l = l_s[hh];
-            const int64_t o = ((int64_t)c * p.total_q + i) * p.Hq + h * G + hh;
-            p.o_part[o * kQ4Dim + od] = l > 0.0f ? acc[k] / l : 0.0f;
-            if (od == 0) p.lse_part[o] = l > 0.0f ? m_s[hh] + log2f(l) : -INFINITY;
-        }
+    for (int r = 0; r < 4; ++r) {
+        const int hh = 4 * g + r;
+        if (hh >= G) continue;
+        const float l = L.lsum[0][hh] + L.lsum[1][hh] + L.lsum[2][hh] + L.lsum[3][hh];
+        const int64_t oi = ((int64_t)c * p.total_q + i) * p.Hq + h * G + hh;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            p.o_part[oi * kQ4Dim + 32 * wave + 16 * j + m16] = l > 0.0f ? o[j][r] / l : 0.0f;
+        if (wave == 0 && m16 == 0) p.lse_part[oi] = l > 0.0f ? m_run[r] + log2f(l) : -INFINITY;
     }
 }
 
