@@ -425,6 +425,8 @@ struct Q4Lds {
     uint16_t P[kQ4MaxGroup * kQ4Pitch];  // [head][token]
     float red[4][kQ4MaxGroup];           // per-wave block maxima
     float lsum[4][kQ4MaxGroup];          // per-wave denominators
+    int lpage[64], lblk[64];             // the valid blocks of a 64-entry window of the list
+    int lcount;
 };
 
 // The packed bytes one thread stages: token t = tid / 2, dims 64 h .. 64 h + 63
@@ -529,101 +531,108 @@ __global__ __launch_bounds__(kQ4Threads) void q4_decode_kernel(Q4DecodeParams p)
         l_run[r] = 0.0f;
     }
 
-    // the next listed block that exists (uniform)
-    auto next_valid = [&](int e, int64_t& page, int& blk) {
-        for (; e < c1; ++e) {
-            blk = tk[e];
-            if (blk < 0 || blk >= n_blocks) continue;
-            page = bt[blk];
-            if (page < 0 || page >= p.num_pages) continue;
-            return e;
+    // The list is walked in windows of 64 entries: wave 0 reads a window's
+    // entries and block-table pages with vector loads and compacts the valid
+    // ones into LDS, so no dependent scalar load sits in front of a block.
+    for (int w0 = c0; w0 < c1; w0 += 64) {
+        __syncthreads();  // every wave is done with the previous window
+        if (wave == 0) {
+            const int e = w0 + lane;
+            int pg = -1, bk = 0;
+            if (e < c1) {
+                bk = tk[e];
+                if (bk >= 0 && bk < n_blocks) {
+                    const int64_t pp = bt[bk];
+                    if (pp >= 0 && pp < p.num_pages) pg = (int)pp;
+                }
+            }
+            const uint64_t vm = __ballot(pg >= 0);
+            const int pos = __popcll(vm & ((1ull << lane) - 1ull));
+            if (pg >= 0) {
+                L.lpage[pos] = pg;
+                L.lblk[pos] = bk;
+            }
+            if (lane == 0) L.lcount = __popcll(vm);
         }
-        return c1;
-    };
-    int64_t page = 0;
-    int blk = 0;
-    int e = next_valid(c0, page, blk);
-    Q4Piece pc;
-    if (e < c1) q4_load_piece(p.pool + (page * (2 * p.Hkv) + 2 * h) * (int64_t)kQ4Slot, tid, pc);
-    while (e < c1) {
-        const int cur_blk = blk;
-        __syncthreads();  // the previous block's LDS reads are done
-        q4_stage_piece(pc, tid, L);
-        int64_t npage = 0;
-        int nblk = 0;
-        const int en = next_valid(e + 1, npage, nblk);
-        if (en < c1) q4_load_piece(p.pool + (npage * (2 * p.Hkv) + 2 * h) * (int64_t)kQ4Slot, tid, pc);
         __syncthreads();
-        const int n_tok = min(kQ4Page, kv_len - cur_blk * kQ4Page);
+        const int n_list = L.lcount;
+        Q4Piece pc;
+        if (n_list > 0) q4_load_piece(p.pool + ((int64_t)L.lpage[0] * (2 * p.Hkv) + 2 * h) * kQ4Slot, tid, pc);
+        for (int k = 0; k < n_list; ++k) {
+            const int cur_blk = L.lblk[k];
+            __syncthreads();  // the previous block's LDS reads are done
+            q4_stage_piece(pc, tid, L);
+            if (k + 1 < n_list)
+                q4_load_piece(p.pool + ((int64_t)L.lpage[k + 1] * (2 * p.Hkv) + 2 * h) * kQ4Slot, tid, pc);
+            __syncthreads();
+            const int n_tok = min(kQ4Page, kv_len - cur_blk * kQ4Page);
 
-        // scores: tokens 32 wave + 16 j + m16 (j = 0, 1), heads 4 g + r
-        float4_t sc[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            sc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
-            const uint16_t* krow = L.K + (32 * wave + 16 * j + m16) * kQ4Pitch + 8 * g;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const half8_t kb = *reinterpret_cast<const half8_t*>(krow + 32 * s);
-                sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, sc[j], 0, 0, 0);
-            }
-        }
-        float bmax[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float mx = -INFINITY;
+            // scores: tokens 32 wave + 16 j + m16 (j = 0, 1), heads 4 g + r
+            float4_t sc[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int t = 32 * wave + 16 * j + m16;
-                const float v = t < n_tok ? sc[j][r] * p.scale_log2 : -INFINITY;
-                sc[j][r] = v;
-                mx = fmaxf(mx, v);
+                sc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+                const uint16_t* krow = L.K + (32 * wave + 16 * j + m16) * kQ4Pitch + 8 * g;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const half8_t kb = *reinterpret_cast<const half8_t*>(krow + 32 * s);
+                    sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, sc[j], 0, 0, 0);
+                }
             }
+            float bmax[4];
 #pragma unroll
-            for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
-            bmax[r] = mx;
-        }
-        if (m16 == 0) {
+            for (int r = 0; r < 4; ++r) {
+                float mx = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) L.red[wave][4 * g + r] = bmax[r];
-        }
-        __syncthreads();
-        float alpha[4];
+                for (int j = 0; j < 2; ++j) {
+                    const int t = 32 * wave + 16 * j + m16;
+                    const float v = t < n_tok ? sc[j][r] * p.scale_log2 : -INFINITY;
+                    sc[j][r] = v;
+                    mx = fmaxf(mx, v);
+                }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int hh = 4 * g + r;
-            const float mb = fmaxf(fmaxf(L.red[0][hh], L.red[1][hh]), fmaxf(L.red[2][hh], L.red[3][hh]));
-            const float mn = fmaxf(m_run[r], mb);
-            alpha[r] = exp2f(m_run[r] - mn);  // 0 while the old max is -inf
-            m_run[r] = mn;
-            float ls = 0.0f;
+                for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
+                bmax[r] = mx;
+            }
+            if (m16 == 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) L.red[wave][4 * g + r] = bmax[r];
+            }
+            __syncthreads();
+            float alpha[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int hh = 4 * g + r;
+                const float mb = fmaxf(fmaxf(L.red[0][hh], L.red[1][hh]), fmaxf(L.red[2][hh], L.red[3][hh]));
+                const float mn = fmaxf(m_run[r], mb);
+                alpha[r] = exp2f(m_run[r] - mn);  // 0 while the old max is -inf
+                m_run[r] = mn;
+                float ls = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float pv = sc[j][r] == -INFINITY ? 0.0f : exp2f(sc[j][r] - mn);
+                    const _Float16 ph = (_Float16)pv;
+                    ls += (float)ph;
+                    L.P[hh * kQ4Pitch + 32 * wave + 16 * j + m16] = __builtin_bit_cast(uint16_t, ph);
+                }
+                l_run[r] = l_run[r] * alpha[r] + ls;
+            }
+            __syncthreads();
+            // O[heads][dims 32 wave + 16 j + m16] = alpha O + P V
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const float pv = sc[j][r] == -INFINITY ? 0.0f : exp2f(sc[j][r] - mn);
-                const _Float16 ph = (_Float16)pv;
-                ls += (float)ph;
-                L.P[hh * kQ4Pitch + 32 * wave + 16 * j + m16] = __builtin_bit_cast(uint16_t, ph);
-            }
-            l_run[r] = l_run[r] * alpha[r] + ls;
-        }
-        __syncthreads();
-        // O[heads][dims 32 wave + 16 j + m16] = alpha O + P V
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+                for (int r = 0; r < 4; ++r) o[j][r] *= alpha[r];
+                const uint16_t* vrow = L.Vt + (32 * wave + 16 * j + m16) * kQ4Pitch + 8 * g;
+                const uint16_t* prow = L.P + m16 * kQ4Pitch + 8 * g;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[j][r] *= alpha[r];
-            const uint16_t* vrow = L.Vt + (32 * wave + 16 * j + m16) * kQ4Pitch + 8 * g;
-            const uint16_t* prow = L.P + m16 * kQ4Pitch + 8 * g;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const half8_t pa = *reinterpret_cast<const half8_t*>(prow + 32 * s);
-                const half8_t vb = *reinterpret_cast<const half8_t*>(vrow + 32 * s);
-                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[j], 0, 0, 0);
+                for (int s = 0; s < 4; ++s) {
+                    const half8_t pa = *reinterpret_cast<const half8_t*>(prow + 32 * s);
+                    const half8_t vb = *reinterpret_cast<const half8_t*>(vrow + 32 * s);
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[j], 0, 0, 0);
+                }
             }
         }
-        e = en;
-        page = npage;
-        blk = nblk;
     }
     // denominators: this lane's shares over the 16 lanes of its head group,
     // then over the four waves
