@@ -54,6 +54,29 @@ def test_decode_mixed_k_beyond_4(gpu, gemv_policy, cb):
     assert rel_l2(got, want) <= TOL
 
 
+def test_decode_mixed_k_split_tail(gpu, gemv_policy):
+    """A decode step whose units outnumber the resident workgroups in both
+    GEMV phases (the one-unit kernel then runs the later units in two halves
+    of the input range), with K 5/6 units computed by the generic kernel and
+    K 7 units zero: every workspace slot of every unit must be written once.
+    128 experts share four packs (pointer tables with repeated entries), so
+    the dense reference needs four dequantisations."""
+    E, H, I, topk, T, cb = 128, 896, 512, 8, 48, 0
+    packs = S.moe_layer(79, 4, H, I, [3, 5, (2, 6, 4), 7])
+    experts = [packs[e % 4] for e in range(E)]
+    dense = [{k: v.astype(np.float32) for k, v in d.items()} for d in _dense(packs, cb)]
+    x = S.activations(80, T, H)
+    ids, w = S.softmax_topk(81, T, E, topk)
+    slots = len(set(ids.ravel().tolist()))
+    resident = 3 * torch.cuda.get_device_properties(gpu).multi_processor_count
+    assert slots * (H // 128) > resident and slots * 2 * (I // 128) > resident
+    want = O.moe_reference(x, ids, w, [dense[e % 4] for e in range(E)])
+    dl = S.to_device(experts, gpu)
+    got = C.moe_forward(torch.from_numpy(x).to(gpu).bfloat16(), torch.from_numpy(ids).to(gpu),
+                        torch.from_numpy(w).to(gpu), dl, E, I, k_tables=dl["k_tables"], codebook=cb)
+    assert rel_l2(got, want) <= TOL
+
+
 @pytest.mark.parametrize("cb", [0, 1, 2])
 def test_prefill_mixed_k_beyond_4(gpu, cb):
     E, H, I, topk, T = len(KS), 256, 384, 4, 40

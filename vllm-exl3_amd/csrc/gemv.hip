@@ -774,7 +774,7 @@ __device__ __forceinline__ void wg_consume(WgStream<K>& rs, int wave, int lane, 
 
 // Everything one projection of one row group needs, shared by all waves.
 struct WgGroup {
-    int rg, nr, arow, row_base, hb_first, j, tiles_n, expert;
+    int rg, nr, arow, row_base, hb_first, nhb, j, tiles_n, expert;
     const void* img;      // rotated activation rows of the streamed projection
     const int* row_map;   // sorted row -> image row (null: the same row)
 };
@@ -826,8 +826,8 @@ __device__ __forceinline__ void wg_projection(const GemvParams& p, const WgGroup
     const int MRB = p.MRB;
     constexpr size_t tile_bytes = 32u * K;
     const size_t row_bytes = (size_t)G.tiles_n * tile_bytes;
-    for (int c0 = 0; c0 < p.R_hb; c0 += p.C_hb) {
-        const int nb = min(p.C_hb, p.R_hb - c0);
+    for (int c0 = 0; c0 < G.nhb; c0 += p.C_hb) {
+        const int nb = min(p.C_hb, G.nhb - c0);
         // trellis bytes of this chunk start moving before the staging below
         WgStream<K> rs;
         const uint8_t* tb = pq.trellis +
@@ -862,10 +862,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     const int nJB = p.out_features >> 7;
     // gate/up: each workgroup streams one of the two projections
     const int nsplit_proj = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
-    const int item = blockIdx.x;
+    int item = blockIdx.x, s, half = -1;
+    if ((MODE == kModeGateUp || MODE == kModeDown) && p.tail_halves > 0) {
+        // units below tail_halves whole, later ones in S parts
+        if (item >= p.tail_halves) {
+            half = (item - p.tail_halves) % p.S;
+            item = p.tail_halves + (item - p.tail_halves) / p.S;
+        }
+        s = half < 0 ? 0 : half;
+    } else {
+        s = (item / nsplit_proj) % p.S;
+        item = item % nsplit_proj + item / nsplit_proj / p.S * nsplit_proj;
+    }
     const int qsel = item % nsplit_proj;
-    const int s = (item / nsplit_proj) % p.S;
-    const int rest = item / nsplit_proj / p.S;
+    const int rest = item / nsplit_proj;
     WgGroup G;
     G.row_map = MODE == kModeGateUp ? p.row_map : nullptr;
     const int jb = rest % nJB;
@@ -920,7 +930,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     const int MRB = p.MRB;
     G.img = (MODE == kModeGateUp && qsel) ? p.x2 : p.x;
     G.tiles_n = p.out_features >> 4;
-    G.hb_first = s * p.R_hb;  // first 128-row input block of this split
+    // input blocks of this unit: the split's, or a half of the whole range
+    G.nhb = half < 0 ? p.R_hb : (half == p.S - 1 ? p.R_hb - half * (p.R_hb / p.S) : p.R_hb / p.S);
+    G.hb_first = half < 0 ? s * p.R_hb : half * (p.R_hb / p.S);
     // LDS: [stage 4 x 1 KB][A: C_hb x 8 x MRB x 16 fp16 | red: 4 waves x MRB
     // x 128 fp32] (red overlays A: the column block's reduction follows its
     // last read of A)
@@ -953,8 +965,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         } else {
             for (int e = tid; e < G.nr * 128; e += kThreads) {
                 const int r = e >> 7, c = e & 127;
-                p.ws[(((int64_t)qsel * p.S + s) * p.n_rows_ws + G.row_base + G.rg + r) * p.out_features +
-                     G.j * 128 + c] = red_sum(red, MRB, r, c);
+                const int64_t o = ((int64_t)qsel * p.S * p.n_rows_ws + G.row_base + G.rg + r) * p.out_features +
+                                  G.j * 128 + c;
+                p.ws[o + (int64_t)s * p.n_rows_ws * p.out_features] = red_sum(red, MRB, r, c);
+                // a whole unit of a split-tail launch: its other slots are zero
+                if ((MODE == kModeGateUp || MODE == kModeDown) && p.tail_halves > 0 && half < 0)
+                    for (int z = 1; z < p.S; ++z) p.ws[o + (int64_t)z * p.n_rows_ws * p.out_features] = 0.0f;
             }
         }
         __syncthreads();
@@ -1010,7 +1026,8 @@ __global__ __launch_bounds__(kThreads) void gemv_anyk_kernel(GemvParams p) {
     uint8_t* st = stage_all[wave];
     for (int s = 0; s < p.S; ++s) {
         float* dst = p.ws + (((int64_t)qsel * p.S + s) * p.n_rows_ws + row_base) * p.out_features + jb * 128;
-        if (!compute) {
+        // a halved-tail launch: slot 0 holds the whole input range, slot 1 zeros
+        if (!compute || (p.tail_halves > 0 && s > 0)) {
             for (int i = tid; i < rows * 128; i += kThreads) dst[(int64_t)(i >> 7) * p.out_features + (i & 127)] = 0.0f;
             continue;
         }
@@ -1393,6 +1410,7 @@ struct PhasePlan {
     int S, R_hb, C_hb, grid;
     int wg;  // 1: one unit per workgroup (gemv_wg_kernel); 0: persistent (gemv_kernel)
     size_t lds;
+    int halves;  // one-unit MoE phase with a halved tail: the whole units (GemvParams::tail_halves)
 };
 
 // One-unit-per-workgroup plan: activation chunk within a 40 KB budget (the
@@ -1415,7 +1433,22 @@ inline int gemv_forced_splits() {
     return v ? std::atoi(v) : 0;
 }
 
-inline PhasePlan plan_phase_wg(int in_f, int out_f, int wg_items, int MRB) {
+// EXL3_GEMV_TAIL_HALVES=0 keeps whole units past the first round of a
+// one-unit MoE phase (tuning; read on every plan, workspace queries included).
+inline int gemv_tail_parts() {
+    const char* v = std::getenv("EXL3_GEMV_TAIL_HALVES");
+    if (v && std::strcmp(v, "0") == 0) return 0;
+    const char* n = std::getenv("EXL3_GEMV_TAIL_PARTS");
+    return n ? std::atoi(n) : 2;
+}
+
+// One-unit-per-workgroup plan.  For a MoE phase whose whole units need a
+// second round of resident workgroups, the units past the first round run as
+// two halves of the input range each (the first-round units write a zero
+// second slot): the SIMD issues from its oldest wave first, so first-round
+// workgroups finish in dispatch order over a wide spread of times, and short
+// late workgroups end the launch sooner than whole ones.
+inline PhasePlan plan_phase_wg(int in_f, int out_f, int wg_items, int MRB, bool moe = false) {
     const int n_hb = in_f / 128, n_j = out_f / 128;
     const int cap = resident_workgroups();
     PhasePlan best = {1, n_hb, pick_chunk_wg(n_hb, MRB), 1, 1, 0};
@@ -1432,6 +1465,13 @@ inline PhasePlan plan_phase_wg(int in_f, int out_f, int wg_items, int MRB) {
             best_t = t;
             best = {S, R_hb, pick_chunk_wg(R_hb, MRB), (int)items, 1, 0};
         }
+    }
+    const int64_t units = (int64_t)wg_items * n_j;
+    const int parts = gemv_tail_parts();
+    if (moe && best.S == 1 && units > cap && parts >= 2 && n_hb >= parts && forced <= 0) {
+        best.S = parts;
+        best.grid = (int)(cap + parts * (units - cap));
+        best.halves = cap;
     }
     const size_t a = (size_t)best.C_hb * 8 * MRB * 16 * 2, r = gemv_red_bytes(MRB);
     best.lds = kWaves * kStageBytes + (a > r ? a : r);
@@ -1463,9 +1503,10 @@ inline int gemv_kernel_policy() {
     return 0;
 }
 
-inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, int wg_items, int MRB) {
+inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, int wg_items, int MRB,
+                            bool moe = false) {
     const int policy = gemv_kernel_policy();
-    if (policy == 1) return plan_phase_wg(in_f, out_f, wg_items, MRB);
+    if (policy == 1) return plan_phase_wg(in_f, out_f, wg_items, MRB, moe);
     const int n_hb = in_f / 128, n_j = out_f / 128;
     const int cap = resident_workgroups();
     PhasePlan best = {1, n_hb, pick_chunk(n_hb, MRB), 1, 0, 0};
@@ -1493,7 +1534,7 @@ inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, i
             best = {S, R_hb, C_hb, grid, 0, 0};
         }
     }
-    if (policy != 2 && best_per_wg < kMinUnitsPerWg) return plan_phase_wg(in_f, out_f, wg_items, MRB);
+    if (policy != 2 && best_per_wg < kMinUnitsPerWg) return plan_phase_wg(in_f, out_f, wg_items, MRB, moe);
     best.lds = gemv_lds_bytes(best.C_hb, MRB);
     return best;
 }
@@ -1530,8 +1571,8 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
     const int64_t est = m.n_routes / m.MRB > m.max_slots ? m.n_routes / m.MRB : m.max_slots;
     const int est_groups = (int)(est < m.max_groups ? est : m.max_groups);
     m.gu = plan_phase((int)hidden, (int)inter, est_groups * m.nproj, m.max_groups * m.nproj,
-                      m.max_slots * m.nproj, m.MRB);
-    m.dn = plan_phase((int)inter, (int)hidden, est_groups, m.max_groups, m.max_slots, m.MRB);
+                      m.max_slots * m.nproj, m.MRB, true);
+    m.dn = plan_phase((int)inter, (int)hidden, est_groups, m.max_groups, m.max_slots, m.MRB, true);
     size_t off = 0;
     m.off_route = off;
     off += align256(sizeof(int) * (2 + 3 * (size_t)m.max_slots + 3 * (size_t)m.n_routes +
@@ -2029,6 +2070,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pg.S = mp.gu.S;
     pg.R_hb = mp.gu.R_hb;
     pg.C_hb = mp.gu.C_hb;
+    pg.tail_halves = mp.gu.halves;
     pg.ws = ws_gu;
     profile_mark(2, st);
     // uniform K over the streamed projections: the lane-linear stage layout
@@ -2046,6 +2088,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pd.S = mp.dn.S;
     pd.R_hb = mp.dn.R_hb;
     pd.C_hb = mp.dn.C_hb;
+    pd.tail_halves = mp.dn.halves;
     pd.ws = ws_d;
     pd.x = img_d;
     pd.x_dtype = kF16;

@@ -113,6 +113,12 @@ struct GemvParams {
     int src_S;
     float limit;
     int act;
+    // One-unit-per-workgroup MoE phases whose units outnumber the resident
+    // workgroups: the first tail_halves units run whole (workgroups 0 ..
+    // tail_halves - 1, writing split slot 0 and zeros into slot 1), every
+    // later unit as two halves of its input range (slots 0 and 1), so the
+    // workgroups that start last are short.  S is 2; 0: plain splits.
+    int tail_halves;
 };
 
 // ---------------------------------------------------------------------------
