@@ -781,34 +781,45 @@ struct WgGroup {
 
 // Copy the rotated activations of a row group for tile rows [kt0, kt0 + nkt)
 // from their image (row-major fp16 rows, MFMA k order inside each 16 inputs)
-// into the LDS operand layout A[kt][MRB][16].  Every load of a batch is
-// issued before its stores, so the copy costs about one L2 round trip.
+// into the LDS operand layout A[kt][MRB][16].  The image row of each of the
+// group's rows is looked up once per batch of rows; each thread then owns
+// 16-byte pieces (tile row, half) and issues the loads of the batch's rows
+// before its stores, so a batch costs about two round trips and no integer
+// division.
 __device__ __forceinline__ void wg_stage_rows(const GemvParams& p, const WgGroup& G, int kt0, int nkt,
                                            uint16_t* A, int tid) {
     typedef __attribute__((address_space(1))) const v4u* gv4c;
+    constexpr int kRowBatch = 4;
     const int MRB = p.MRB;
-    const int pieces = G.nr * nkt * 2;  // 16-byte pieces, row-major
     const uint16_t* img = reinterpret_cast<const uint16_t*>(G.img);
-    constexpr int kBatch = 8;
-    for (int b0 = 0; b0 < pieces; b0 += kThreads * kBatch) {
-        v4u v[kBatch];
+    const int npc = nkt * 2;  // 16-byte pieces per row
+    // a zero the compiler cannot see through: the row map is read with vector
+    // loads (one request per wave, no scalar registers held across the copy)
+    int vzero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+    for (int r0 = 0; r0 < G.nr; r0 += kRowBatch) {
+        int64_t src[kRowBatch];
+        const int64_t srow0 = G.row_base + G.rg;
+        if (G.row_map) {
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int pc = b0 + b * kThreads + tid;
-            if (pc < pieces) {
-                const int h = pc & 1, kt = (pc >> 1) % nkt, r = (pc >> 1) / nkt;
-                const int64_t srow = G.row_base + G.rg + r;
-                const int64_t row = G.row_map ? G.row_map[srow] : srow;
-                v[b] = *(gv4c)(img + row * p.x_stride + (int64_t)(kt0 + kt) * 16 + 8 * h);
-            }
+            for (int b = 0; b < kRowBatch; ++b)
+                src[b] = (int64_t)G.row_map[srow0 + min(r0 + b, G.nr - 1) + vzero];
+        } else {
+#pragma unroll
+            for (int b = 0; b < kRowBatch; ++b) src[b] = srow0 + min(r0 + b, G.nr - 1);
         }
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int pc = b0 + b * kThreads + tid;
-            if (pc < pieces) {
-                const int h = pc & 1, kt = (pc >> 1) % nkt, r = (pc >> 1) / nkt;
-                *reinterpret_cast<v4u*>(A + (kt * MRB + r) * 16 + 8 * h) = v[b];
-            }
+        for (int b = 0; b < kRowBatch; ++b) src[b] = src[b] * p.x_stride + (int64_t)kt0 * 16;
+        for (int c = tid; c < npc; c += kThreads) {
+            const int64_t off = (int64_t)(c >> 1) * 16 + 8 * (c & 1);
+            v4u v[kRowBatch];
+#pragma unroll
+            for (int b = 0; b < kRowBatch; ++b)
+                if (r0 + b < G.nr) v[b] = *(gv4c)(img + src[b] + off);
+#pragma unroll
+            for (int b = 0; b < kRowBatch; ++b)
+                if (r0 + b < G.nr)
+                    *reinterpret_cast<v4u*>(A + ((c >> 1) * MRB + r0 + b) * 16 + 8 * (c & 1)) = v[b];
         }
     }
 }
