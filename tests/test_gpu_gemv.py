@@ -49,6 +49,29 @@ def test_gemm_config0_full_size(gpu, gemv_policy, m):
     assert rel_l2(got16, want) <= TOL
 
 
+@pytest.mark.parametrize("m,xdt", [(1, torch.bfloat16), (3, torch.float16), (4, torch.float32),
+                                    (5, torch.bfloat16)])
+def test_linear_raw_rows_vs_rotation_launch(gpu, gemv_policy, monkeypatch, m, xdt):
+    """Up to 4 rows the linear GEMV rotates its own input blocks while staging
+    them; EXL3_LINEAR_RAW=0 keeps the rotation launch.  Both against the
+    oracle and each other, with a bias (5 rows always take the launch)."""
+    in_f, out_f = 2048, 640
+    lin = S.linear(4100 + m, in_f, out_f, 3)
+    x = S.activations(9 + m, m, in_f)
+    bias = np.random.default_rng(m).standard_normal(out_f).astype(np.float16)
+    w = O.dequant(lin["trellis"], lin["suh"], lin["svh"], 3, 0)
+    want = O.gemv(x, w) + bias.astype(np.float32)
+    args = (torch.from_numpy(x).to(gpu).to(xdt), torch.from_numpy(lin["trellis"]).to(gpu),
+            torch.from_numpy(lin["suh"]).to(gpu), torch.from_numpy(lin["svh"]).to(gpu), 3, False)
+    b = torch.from_numpy(bias).to(gpu)
+    raw = C.exl3_gemm(*args, codebook=0, out_dtype=torch.float32, bias=b)
+    monkeypatch.setenv("EXL3_LINEAR_RAW", "0")
+    img = C.exl3_gemm(*args, codebook=0, out_dtype=torch.float32, bias=b)
+    torch.cuda.synchronize()
+    assert rel_l2(raw, want) <= TOL and rel_l2(img, want) <= TOL
+    assert rel_l2(raw, img.cpu().numpy()) <= TOL
+
+
 def test_exl3_gemv_contract(gpu):
     lin = S.linear(11, 256, 256, 3)
     x = torch.from_numpy(S.activations(2, 4, 256)).to(gpu).half()

@@ -616,6 +616,7 @@ __global__ __launch_bounds__(256) void linear_out_kernel(const float* z, int N, 
 // loads step t + 4.
 constexpr int kFatThreads = 768;
 constexpr int kFatProducers = 4;  // waves that load, decode and stage; the other eight run the MFMAs
+static_assert(kFatThreads / 64 == 3 * kFatProducers, "every third wave is a producer");
 constexpr int kStages = 3;
 constexpr int kFatLds = kStages * (kABytes + kBBytes);  // 96 KB
 

@@ -824,6 +824,44 @@ __device__ __forceinline__ void wg_stage_rows(const GemvParams& p, const WgGroup
     }
 }
 
+// Rotated activations of a plain linear's rows for tile rows [kt0, kt0 + nkt)
+// (whole 128-input blocks), computed from the raw input rows: each wave takes
+// (row, block) units in turn, four at a time with all their loads issued
+// first, and computes fp16(had128(x * suh) / sqrt(128)) as the rotation
+// kernel does, stored in the LDS operand layout A[kt][MRB][16] (the 16
+// inputs of a tile row in MFMA k order).  Used for a few rows, where
+// rotating in every workgroup costs less than a separate launch.
+__device__ __forceinline__ void wg_stage_rotate(const GemvParams& p, const WgGroup& G, int kt0, int nkt,
+                                             uint16_t* A, int wave, int lane) {
+    constexpr int kBatch = 4;
+    const int MRB = p.MRB;
+    const int nb = nkt >> 3, hb0 = kt0 >> 3, nu = G.nr * nb;
+    for (int u0 = wave; u0 < nu; u0 += kWaves * kBatch) {
+        float v[kBatch][2], su[kBatch][2];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int u = min(u0 + i * kWaves, nu - 1);
+            const int r = u / nb, blk = hb0 + u - (u / nb) * nb;
+            const int64_t base = (int64_t)(G.row_base + G.rg + r) * p.x_stride + (int64_t)blk * 128;
+            v[i][0] = load_act(p.x, p.x_dtype, base + lane);
+            v[i][1] = load_act(p.x, p.x_dtype, base + lane + 64);
+            su[i][0] = (float)bits_to_half(p.w_suh[blk * 128 + lane]);
+            su[i][1] = (float)bits_to_half(p.w_suh[blk * 128 + lane + 64]);
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int u = u0 + i * kWaves;
+            if (u >= nu) break;  // wave-uniform
+            const int r = u / nb, b = u - r * nb;
+            float v0 = v[i][0] * su[i][0], v1 = v[i][1] * su[i][1];
+            had128(v0, v1, lane);
+            const int c0 = lane, c1 = lane + 64;
+            A[((b * 8 + (c0 >> 4)) * MRB + r) * 16 + pi_inv(c0 & 15)] = half_to_bits(f32_to_f16_rne(v0 * kHadNorm));
+            A[((b * 8 + (c1 >> 4)) * MRB + r) * 16 + pi_inv(c1 & 15)] = half_to_bits(f32_to_f16_rne(v1 * kHadNorm));
+        }
+    }
+}
+
 // Stage the activations of one projection for chunk [c0, c0 + nb) of
 // 128-row blocks, stream its tiles, and leave each wave's partial sums in
 // red[wave][row][128].  acc lives only inside this K-specialised routine.
@@ -846,7 +884,10 @@ __device__ __forceinline__ void wg_projection(const GemvParams& p, const WgGroup
         wg_prefetch<K>(rs, tb, row_bytes, nb * 8, wave, lane);
         if (restage) {
             __syncthreads();
-            wg_stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
+            if (p.x_raw)
+                wg_stage_rotate(p, G, (G.hb_first + c0) * 8, nb * 8, A, wave, lane);
+            else
+                wg_stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
             __syncthreads();
         }
         wg_consume<K, CB>(rs, wave, lane, stage, A, MRB, G.arow, acc);
@@ -1608,6 +1649,19 @@ struct LinPlan {
     size_t off_img, total;
 };
 
+// Up to kRawRows rows the linear GEMV's workgroups rotate their own input
+// blocks while staging them (no rotation launch, no image in HBM); more rows
+// are rotated once by rotate_rows_kernel, since every column block would
+// repeat the rotation.  EXL3_LINEAR_RAW=0 keeps the rotation launch
+// (tuning and tests; read on every call).
+constexpr int64_t kRawRows = 4;
+
+inline bool linear_raw_rows(int64_t m) {
+    const char* v = std::getenv("EXL3_LINEAR_RAW");
+    if (v && std::strcmp(v, "0") == 0) return false;
+    return m <= kRawRows;
+}
+
 inline LinPlan plan_linear(int64_t m, int64_t in_f, int64_t out_f) {
     LinPlan lp;
     lp.MRB = (int)(m < kMaxMRB ? m : kMaxMRB);
@@ -1779,9 +1833,16 @@ EXL3_API int exl3_linear(const void* x, int x_dtype, int64_t m, const int16_t* t
     p.ws = reinterpret_cast<float*>(workspace);
     profile_begin_call();
     profile_mark(0, st);
-    const int64_t rot_units = m * (in_f / 128);
-    rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
-    EXL3_LAUNCHED();
+    const bool raw = linear_raw_rows(m) && lp.ph.wg;  // the one-unit kernel stages raw rows
+    if (raw) {
+        p.x = x;
+        p.x_dtype = x_dtype;
+        p.x_raw = 1;
+    } else {
+        const int64_t rot_units = m * (in_f / 128);
+        rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
+        EXL3_LAUNCHED();
+    }
     profile_mark(1, st);
     EXL3_HIP(launch_gemv<kModeLinear>(codebook, (int)K, lp.ph, st, p));
     profile_mark(2, st);

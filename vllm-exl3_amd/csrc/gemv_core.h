@@ -113,6 +113,10 @@ struct GemvParams {
     int src_S;
     float limit;
     int act;
+    // Linear mode, one unit per workgroup and one split: x holds the raw
+    // input rows (x_dtype) and each workgroup rotates the blocks it streams
+    // into LDS itself (one launch: no image, no split partials).
+    int x_raw;
     // One-unit-per-workgroup MoE phases whose units outnumber the resident
     // workgroups: the first tail_halves units run whole (workgroups 0 ..
     // tail_halves - 1, writing split slot 0 and zeros into slot 1), every
