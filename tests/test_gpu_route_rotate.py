@@ -1,7 +1,10 @@
-"""GPU parity of the decode step with routing and the gate/up input rotation
-in one launch (the GEMV stages its sorted rows through the router's sorted
-row -> route map) against the oracle and against separate route and rotate
-launches (EXL3_MOE_ROUTE_ROTATE=0) on the same inputs: uniform-K layers,
+"""GPU parity of the decode step's three routing forms on the same inputs:
+inline routing (steps of at most 64 routes: every gate/up GEMV workgroup
+routes the step itself and rotates its rows from x; workgroup 0 writes the
+router's tables), routing and the gate/up input rotation in one launch
+(EXL3_MOE_INLINE_ROUTE=0; the GEMV stages its sorted rows through the
+router's sorted row -> route map), and separate route and rotate launches
+(also EXL3_MOE_ROUTE_ROTATE=0), against the oracle: uniform-K layers,
 decode batch sizes, silu / clamped silu / SwiGLU-OAI / gateless relu2, int32
 and int64 ids, sentinel ids, padded rows (n_valid), fp16/bf16/fp32 outputs.
 Relative L2 <= 2e-3 against the oracle; the two launch sequences compute the
@@ -20,8 +23,10 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-def _run(monkeypatch, fused, *a, **kw):
-    monkeypatch.setenv("EXL3_MOE_ROUTE_ROTATE", "1" if fused else "0")
+def _run(monkeypatch, mode, *a, **kw):
+    """mode: "inline", True (route + rotate launch) or False (separate launches)."""
+    monkeypatch.setenv("EXL3_MOE_INLINE_ROUTE", "1" if mode == "inline" else "0")
+    monkeypatch.setenv("EXL3_MOE_ROUTE_ROTATE", "0" if mode is False else "1")
     out = C.moe_forward(*a, **kw)
     torch.cuda.synchronize()
     return out
@@ -47,6 +52,7 @@ def test_route_rotate_matches_oracle_and_separate_launches(gpu, monkeypatch, cas
     if T > 2:
         ids[1, 0] = -1          # invalid id
         ids[2, -1] = E + 3      # non-local id
+        ids[0, 1] = ids[0, 0]   # one token routed twice to an expert
     act_name = "silu" if gateless else act
     want = O.moe_reference(x, ids, w, dense_cpu(experts, cb), limit=limit, act=act_name)
     dl = S.to_device(experts, gpu)
@@ -54,12 +60,14 @@ def test_route_rotate_matches_oracle_and_separate_launches(gpu, monkeypatch, cas
     args = (torch.from_numpy(x).to(gpu).bfloat16(), torch.from_numpy(ids).to(gpu).to(torch.int32),
             torch.from_numpy(w).to(gpu), dl, E, I)
     kw = dict(K=(K, K, K), codebook=cb, gateless=gateless, act=act_id, swiglu_limit=limit)
+    inl = _run(monkeypatch, "inline", *args, **kw)
     fused = _run(monkeypatch, True, *args, **kw)
     six = _run(monkeypatch, False, *args, **kw)
     assert rel_l2(fused, want) <= TOL
     assert torch.equal(fused, six)
-    again = _run(monkeypatch, True, *args, **kw)
-    assert torch.equal(fused, again), "the decode step must be deterministic"
+    assert torch.equal(inl, fused)
+    again = _run(monkeypatch, "inline", *args, **kw)
+    assert torch.equal(inl, again), "the decode step must be deterministic"
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
@@ -80,14 +88,19 @@ def test_route_rotate_padded_and_routeless_rows(gpu, monkeypatch, out_dtype):
     out2 = torch.full((T, H), 5.0, dtype=out_dtype, device=gpu)
     sep = _run(monkeypatch, False, *args, K=(4, 4, 4), codebook=1, n_valid=n_valid, out=out2)
     assert torch.equal(got, sep)
+    out3 = torch.full((T, H), 5.0, dtype=out_dtype, device=gpu)
+    inl = _run(monkeypatch, "inline", *args, K=(4, 4, 4), codebook=1, n_valid=n_valid, out=out3)
+    assert torch.equal(inl, sep)
     assert torch.count_nonzero(got[n_live:]) == 0 and torch.count_nonzero(got[3]) == 0
     want = O.moe_reference(x[:n_live], ids[:n_live], w[:n_live], dense_cpu(experts, 1))
     tol = TOL if out_dtype == torch.float32 else TOL + 4e-3
     assert rel_l2(got[:n_live].float(), want) <= tol
 
 
-def test_route_rotate_graph_replay(gpu, monkeypatch):
+@pytest.mark.parametrize("inline", [True, False])
+def test_route_rotate_graph_replay(gpu, monkeypatch, inline):
     monkeypatch.setenv("EXL3_MOE_ROUTE_ROTATE", "1")
+    monkeypatch.setenv("EXL3_MOE_INLINE_ROUTE", "1" if inline else "0")
     T, E, H, I, topk = 4, 8, 256, 384, 4
     experts = S.moe_layer(320, E, H, I, 3)
     dl = S.to_device(experts, gpu)

@@ -777,7 +777,90 @@ struct WgGroup {
     int rg, nr, arow, row_base, hb_first, nhb, j, tiles_n, expert;
     const void* img;      // rotated activation rows of the streamed projection
     const int* row_map;   // sorted row -> image row (null: the same row)
+    int rpos;             // inline routing: sorted row of this lane's route (-1: dropped)
 };
+
+// Routing of a decode step with at most 64 routes by one wave, lane r
+// holding route r = t * topk + k: the router's stable order by local expert
+// (route_impl.h; dropped routes: ids outside [0, n_local) and rows at or past
+// *n_valid), computed with shuffles instead of a sort.
+struct WaveRoute {
+    int key;       // local expert; n_local when dropped
+    int pos;       // sorted row; -1 when dropped
+    int cnt;       // routes of this lane's expert
+    int slot;      // slot of this lane's expert (experts ascending)
+    int tiles;     // row tiles of the slot (first route of an expert), else 0
+    int mt0;       // first row tile of the slot (first route of an expert)
+    bool first;    // first route of its expert in route order
+    int n_active;  // slots
+    int n_tiles;   // row tiles
+};
+
+__device__ __forceinline__ WaveRoute wave_route(const GemvParams& p, int lane) {
+    WaveRoute w;
+    const int n = p.r_n_routes, nl = p.r_n_local;
+    const int live = p.r_n_valid ? min(n, max(0, p.r_n_valid[0]) * p.r_topk) : n;
+    w.key = lane < n ? route_key(p.r_ids, p.r_ids_i64, lane, live, nl) : nl;
+    const bool valid = w.key < nl;
+    int lt = 0, eqb = 0, cnt = 0;
+    for (int j = 0; j < n; ++j) {
+        const int kj = __shfl(w.key, j, 64);
+        lt += kj < w.key;
+        eqb += (kj == w.key) && (j < lane);
+        cnt += kj == w.key;
+    }
+    w.first = valid && eqb == 0;
+    w.pos = valid ? lt + eqb : -1;
+    w.cnt = cnt;
+    w.tiles = w.first ? (cnt + p.MRB - 1) / p.MRB : 0;
+    const uint64_t fm = __ballot(w.first);
+    int slot = 0, mt0 = 0;
+    for (int j = 0; j < n; ++j) {
+        const int kj = __shfl(w.key, j, 64), tj = __shfl(w.tiles, j, 64);
+        const bool before = ((fm >> j) & 1ull) && kj < w.key;
+        slot += before;
+        mt0 += before ? tj : 0;
+    }
+    w.slot = slot;
+    w.mt0 = mt0;
+    w.n_active = __popcll(fm);
+    int tot = w.tiles;
+    for (int d = 32; d; d >>= 1) tot += __shfl_xor(tot, d, 64);
+    w.n_tiles = tot;
+    return w;
+}
+
+// The router's tables (RouteOut, row tiles of MRB rows) from one wave's
+// routing, for the kernels after the gate/up GEMV.
+__device__ __forceinline__ void write_route_tables(const GemvParams& p, const WaveRoute& w, int lane) {
+    const RouteOut& o = p.ro;
+    if (lane < p.r_n_routes) {
+        o.route_pos[lane] = w.pos;
+        if (w.pos >= 0) {
+            o.row_token[w.pos] = lane / p.r_topk;
+            o.row_expert[w.pos] = w.key;
+            if (o.row_route) o.row_route[w.pos] = lane;
+        }
+    }
+    if (w.first) {
+        o.slot_expert[w.slot] = w.key;
+        o.slot_start[w.slot] = w.pos;
+        o.slot_rows[w.slot] = w.cnt;
+        if (o.n_mtiles) {
+            for (int k = 0; k < w.tiles; ++k) {
+                o.mt_slot[w.mt0 + k] = w.slot;
+                if (o.mt_expert) o.mt_expert[w.mt0 + k] = w.key;
+                o.mt_row0[w.mt0 + k] = k * p.MRB;
+            }
+        }
+    }
+    const int kept = __popcll(__ballot(w.pos >= 0));
+    if (lane == 0) {
+        o.n_active[0] = w.n_active;
+        if (o.n_mtiles) o.n_mtiles[0] = w.n_tiles;
+        if (o.n_sorted) o.n_sorted[0] = kept;
+    }
+}
 
 // Copy the rotated activations of a row group for tile rows [kt0, kt0 + nkt)
 // from their image (row-major fp16 rows, MFMA k order inside each 16 inputs)
@@ -831,8 +914,17 @@ __device__ __forceinline__ void wg_stage_rows(const GemvParams& p, const WgGroup
 // kernel does, stored in the LDS operand layout A[kt][MRB][16] (the 16
 // inputs of a tile row in MFMA k order).  Used for a few rows, where
 // rotating in every workgroup costs less than a separate launch.
+// Input row of the group's row r: the sorted row itself for a linear; with
+// inline routing, the token of the route at that sorted row.
+__device__ __forceinline__ int64_t raw_row(const GemvParams& p, const WgGroup& G, int r) {
+    const int srow = G.row_base + G.rg + r;
+    if (!p.inline_route) return srow;
+    const uint64_t m = __ballot(G.rpos == srow);
+    return (int64_t)((__ffsll((unsigned long long)m) - 1) / p.r_topk);
+}
+
 __device__ __forceinline__ void wg_stage_rotate(const GemvParams& p, const WgGroup& G, int kt0, int nkt,
-                                             uint16_t* A, int wave, int lane) {
+                                             uint16_t* A, const uint16_t* suh, int wave, int lane) {
     constexpr int kBatch = 4;
     const int MRB = p.MRB;
     const int nb = nkt >> 3, hb0 = kt0 >> 3, nu = G.nr * nb;
@@ -842,11 +934,11 @@ __device__ __forceinline__ void wg_stage_rotate(const GemvParams& p, const WgGro
         for (int i = 0; i < kBatch; ++i) {
             const int u = min(u0 + i * kWaves, nu - 1);
             const int r = u / nb, blk = hb0 + u - (u / nb) * nb;
-            const int64_t base = (int64_t)(G.row_base + G.rg + r) * p.x_stride + (int64_t)blk * 128;
+            const int64_t base = raw_row(p, G, r) * p.x_stride + (int64_t)blk * 128;
             v[i][0] = load_act(p.x, p.x_dtype, base + lane);
             v[i][1] = load_act(p.x, p.x_dtype, base + lane + 64);
-            su[i][0] = (float)bits_to_half(p.w_suh[blk * 128 + lane]);
-            su[i][1] = (float)bits_to_half(p.w_suh[blk * 128 + lane + 64]);
+            su[i][0] = (float)bits_to_half(suh[blk * 128 + lane]);
+            su[i][1] = (float)bits_to_half(suh[blk * 128 + lane + 64]);
         }
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
@@ -885,7 +977,7 @@ __device__ __forceinline__ void wg_projection(const GemvParams& p, const WgGroup
         if (restage) {
             __syncthreads();
             if (p.x_raw)
-                wg_stage_rotate(p, G, (G.hb_first + c0) * 8, nb * 8, A, wave, lane);
+                wg_stage_rotate(p, G, (G.hb_first + c0) * 8, nb * 8, A, pq.suh, wave, lane);
             else
                 wg_stage_rows(p, G, (G.hb_first + c0) * 8, nb * 8, A, threadIdx.x);
             __syncthreads();
@@ -951,6 +1043,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
                               (int64_t)(G.row_base + (e >> 7)) * p.out_stride + jb * 128 + (e & 127), 0.0f);
             return;
         }
+    } else if (MODE == kModeGateUp && p.inline_route) {
+        // route the step in every wave; workgroup 0 publishes the tables
+        const WaveRoute wr = wave_route(p, lane);
+        if (blockIdx.x == 0 && wave == 0) write_route_tables(p, wr, lane);
+        if (slot >= wr.n_active) return;  // workgroup-uniform, before any barrier
+        const uint64_t m = __ballot(wr.first && wr.slot == slot);
+        const int L = __ffsll((unsigned long long)m) - 1;
+        G.expert = __builtin_amdgcn_readfirstlane(__shfl(wr.key, L, 64));
+        G.row_base = __builtin_amdgcn_readfirstlane(__shfl(wr.pos, L, 64));
+        rows = __builtin_amdgcn_readfirstlane(__shfl(wr.cnt, L, 64));
+        G.rpos = wr.pos;
     } else {
         if (slot >= *p.n_active) return;
         G.expert = p.slot_expert[slot];
@@ -1593,6 +1696,15 @@ inline PhasePlan plan_phase(int in_f, int out_f, int est_items, int max_items, i
 
 // EXL3_MOE_ROUTE_ROTATE=0 keeps routing and the input rotation in separate
 // launches (for comparisons; read on every call).
+// EXL3_MOE_INLINE_ROUTE=0 keeps the routing launch for decode steps of at
+// most 64 routes (whose gate/up GEMV otherwise routes the step itself).
+inline bool moe_inline_route_allowed() {
+    const char* v = std::getenv("EXL3_MOE_INLINE_ROUTE");
+    return !(v && std::strcmp(v, "0") == 0);
+}
+constexpr int kInlineRouteMax = 64;     // routes one wave holds
+constexpr int kInlineRouteBlocks = 4;   // input blocks per gate/up workgroup
+
 inline bool moe_route_rotate_allowed() {
     const char* v = std::getenv("EXL3_MOE_ROUTE_ROTATE");
     return !(v && v[0] == '0');
@@ -2039,9 +2151,19 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     uint16_t* img_gu1 = img_gu + (size_t)mp.n_routes * hidden;
     // Route and rotate in one launch when the gate/up GEMV stages its rows
     // through the sorted row -> route map (one unit per workgroup, uniform K).
-    const bool route_rotate = moe_route_rotate_allowed() && mp.gu.wg && n_local <= kRouteMaxLocal &&
-                              !kt[0] && !kt[1];
-    if (route_rotate) {
+    // Decode steps of at most 64 routes whose gate/up workgroups stream at
+    // most kInlineRouteBlocks input blocks each: the gate/up GEMV routes the
+    // step in every workgroup and rotates its rows from x (no routing
+    // launch; with longer splits every column block repeating the rotation
+    // costs more than the launch, C1 T = 4 +1.5 µs against T = 1 -3 µs).
+    const bool inline_route = moe_inline_route_allowed() && mp.gu.wg && mp.n_routes <= kInlineRouteMax &&
+                              mp.gu.R_hb <= kInlineRouteBlocks && n_local <= kRouteMaxLocal && !kt[0] &&
+                              !kt[1];
+    const bool route_rotate = !inline_route && moe_route_rotate_allowed() && mp.gu.wg &&
+                              n_local <= kRouteMaxLocal && !kt[0] && !kt[1];
+    if (inline_route) {
+        ro.row_route = reinterpret_cast<int*>(ws + mp.off_aux);
+    } else if (route_rotate) {
         static const hipError_t attr = [] {
             hipError_t e = hipFuncSetAttribute((const void*)route_rotate_kernel,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2110,7 +2232,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
 
     // gate/up input rows, rotated once per route and projection
     profile_mark(1, st);
-    if (!route_rotate) {
+    if (!route_rotate && !inline_route) {
         RotateArgs ra = {};
         ra.x = x;
         ra.x_dtype = x_dtype;
@@ -2137,6 +2259,20 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pg.row_map = route_rotate ? ro.row_route : nullptr;
     pg.x_dtype = kF16;
     pg.x_stride = hidden;
+    if (inline_route) {
+        pg.x = x;
+        pg.x2 = x;
+        pg.x_dtype = x_dtype;
+        pg.x_raw = 1;
+        pg.inline_route = 1;
+        pg.r_ids = ids;
+        pg.r_ids_i64 = (int)ids_dtype;
+        pg.r_n_routes = mp.n_routes;
+        pg.r_topk = (int)topk;
+        pg.r_n_local = (int)n_local;
+        pg.r_n_valid = n_valid;
+        pg.ro = ro;
+    }
     pg.in_features = (int)hidden;
     pg.out_features = (int)inter;
     pg.S = mp.gu.S;

@@ -32,6 +32,7 @@
 #pragma once
 
 #include "exl3_common.h"
+#include "route.h"
 
 namespace exl3 {
 
@@ -123,6 +124,16 @@ struct GemvParams {
     // later unit as two halves of its input range (slots 0 and 1), so the
     // workgroups that start last are short.  S is 2; 0: plain splits.
     int tail_halves;
+    // Gate/up of a decode step with at most 64 routes, one unit per
+    // workgroup: every wave routes the step itself (ids -> stable order by
+    // expert, as the router does) and rotates its rows from the raw input
+    // (x_raw); workgroup 0 writes the router's tables (ro) for the kernels
+    // that follow.  No routing launch.
+    int inline_route;
+    const void* r_ids;
+    int r_ids_i64, r_n_routes, r_topk, r_n_local;
+    const int32_t* r_n_valid;
+    RouteOut ro;
 };
 
 // ---------------------------------------------------------------------------
