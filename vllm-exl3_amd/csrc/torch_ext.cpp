@@ -611,6 +611,8 @@ Tensor ngram_dequant_rows(const Tensor& packed, int64_t bits, const Tensor& head
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    // torch's Python types (dtype defaults below) must exist before the defs
+    py::module_::import("torch");
     m.doc() = "EXL3 routed-expert path on MI355X: the reference's native module surface over the C ABI";
     // Module attributes the plugin gates on (csrc/bindings.cpp:243-257).
     m.attr("P2B_MOE_ABI_VERSION") = 4;
