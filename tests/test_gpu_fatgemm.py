@@ -53,6 +53,32 @@ def test_fat_gemm_large_m_deterministic(gpu):
     assert rel_l2(out1, want) <= TOL
 
 
+@pytest.mark.parametrize("K,cb", [(2, 0), (3, 1), (4, 2)])
+def test_fat_gemm_helper_waves_bit_exact(gpu, monkeypatch, K, cb):
+    """Row tiles of at most 128 rows let the second row half's MFMA waves
+    decode half of each B tile (EXL3_FAT_HELPERS=0: the producers decode it
+    all); the decoded values, and so the outputs, are the same bit for bit.
+    700 rows: two full tiles, one of 188 rows and a last tile of 0..128-row
+    sizes across the grid of column tiles."""
+    M, kin, n = 700, 384, 640
+    lin = S.linear(90 + K, kin, n, K)
+    a16 = S.activations(6, M, kin).astype(np.float16)
+    a = torch.from_numpy(a16).to(gpu)
+    t = torch.from_numpy(lin["trellis"]).to(gpu)
+    sv = torch.from_numpy(lin["svh"]).to(gpu)
+    outs = []
+    for helpers in ("1", "0"):
+        monkeypatch.setenv("EXL3_FAT_HELPERS", helpers)
+        for m in (700, 100, 33):
+            o = torch.empty((m, n), dtype=torch.float32, device=gpu)
+            C.exl3_fat_gemm(a[:m].contiguous(), t, o, sv, K, cb == 1, cb == 2)
+            outs.append(o)
+    torch.cuda.synchronize()
+    for x, y in zip(outs[:3], outs[3:]):
+        assert torch.equal(x, y)
+    assert rel_l2(outs[0], _want(a16, lin, cb)) <= TOL
+
+
 def test_fat_gemm_scatter(gpu):
     M, kin, n, T = 40, 256, 256, 64
     lin = S.linear(88, kin, n, 3)

@@ -39,6 +39,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 
 namespace exl3 {
 namespace {
@@ -89,6 +91,9 @@ struct FatParams {
     const int8_t* ktab2;
     int kuni2;
     void* out2;
+    // tiles of at most 128 rows let their idle MFMA waves decode half of B
+    // (set by the launch; EXL3_FAT_HELPERS=0 turns it off)
+    int helpers;
 };
 
 // Decoded (lo, hi) half pair of one window for the sum-of-halves codebooks,
@@ -640,7 +645,8 @@ __device__ __forceinline__ void decode_group_half(const uint32_t (&w)[K + 1], ui
 // bytes of A and decodes one 32-weight group (both column halves) into the
 // B stage.  One barrier per k-step, three stages, as the consumers.
 template <int CB, int K>
-__device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps) {
+__device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps,
+                                             bool helped) {
     constexpr int tile_bytes = 32 * K;
     const int pt = (threadIdx.x >> 6) / 3 * 64 + (threadIdx.x & 63);  // 0..255
     const int tiles_n = p.N >> 4;
@@ -683,7 +689,7 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[r][jj];
         decode_group_half<K, CB, 0>(gw[r], B, col0, 2 * tr);
-        decode_group_half<K, CB, 1>(gw[r], B, col0, 2 * tr);
+        if (!helped) decode_group_half<K, CB, 1>(gw[r], B, col0, 2 * tr);
     };
     // prologue: stages 0, 1 hold steps 0, 1; the registers hold steps 2, 3,
     // issued in the loop's order (register set 0 before set 1) so that the
@@ -702,6 +708,62 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             stage(st_cur == 0 ? 2 : st_cur - 1, u);  // step t + u + 2 into stage (t + u + 2) % 3
+            load(t + u + 4, u);
+            lds_barrier();
+            st_cur = st_cur == 2 ? 0 : st_cur + 1;
+        }
+    }
+}
+
+// Helper waves: in a tile of at most 128 rows the four MFMA waves of the
+// second row half have no rows; they decode the second column half of every
+// 32-weight group instead (the producers decode the first), with the
+// producers' loads, stages and barriers (one per k-step, the same count).
+// pt: the thread's group, as the producers number them (0..255).
+template <int CB, int K>
+__device__ __forceinline__ void fat_helper(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps,
+                                           int pt) {
+    constexpr int tile_bytes = 32 * K;
+    const int tiles_n = p.N >> 4;
+    const int t_idx = pt >> 3, g = pt & 7;
+    const int tr = t_idx >> 4, tc = t_idx & 15;
+    const int tcols = min(16, tiles_n - ft.nt * 16);
+    const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(ft.trellis + (size_t)ft.nt * 16 * tile_bytes), (short)0, 0x7FFFFFFF, 0x00020000);
+    const int t_voff = (tr * tiles_n + min(tc, tcols - 1)) * tile_bytes;
+    const int step_bytes = 2 * tiles_n * tile_bytes;
+    int w_voff[K + 1];
+#pragma unroll
+    for (int j = 0; j < K + 1; ++j) {
+        const int idx = g * K - 1 + j;
+        w_voff[j] = t_voff + 4 * (idx < 0 ? idx + 8 * K : idx);
+    }
+    const int col0 = tc * 16 + g;
+    uint32_t gw[2][K + 1];
+    auto load = [&](int t, int r) {
+        const int so = min(t, nsteps - 1);
+#pragma unroll
+        for (int j = 0; j < K + 1; ++j)
+            gw[r][j] = __builtin_amdgcn_raw_buffer_load_b32(trs, w_voff[j], so * step_bytes, 0);
+    };
+    auto stage = [&](int st, int r) {
+        uint8_t* B = lds + kStages * kABytes + st * kBBytes;
+        decode_group_half<K, CB, 1>(gw[r], B, col0, 2 * tr);
+    };
+    load(0, 0);
+    load(1, 1);
+    stage(0, 0);
+    stage(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load(2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(3, 1);
+    lds_barrier();
+    int st_cur = 0;
+    for (int t = 0; t < nsteps; t += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            stage(st_cur == 0 ? 2 : st_cur - 1, u);
             load(t + u + 4, u);
             lds_barrier();
             st_cur = st_cur == 2 ? 0 : st_cur + 1;
@@ -778,17 +840,25 @@ __device__ __forceinline__ void fat_consumer(const FatParams& p, const FatTile& 
     }
 }
 
+__device__ __forceinline__ bool fat_helpers_on(const FatParams& p) { return p.helpers != 0; }
+
 template <int CB, int K>
 __device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft, uint8_t* lds) {
     const int nsteps = p.K_in / kTK;  // a multiple of 4 (K_in is a multiple of 128)
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    // at most 128 rows: the second row half's MFMA waves help decode B
+    const bool helped = ft.rows_valid <= 128 && fat_helpers_on(p);
     if (w % 3 == 0) {  // waves 0, 3, 6, 9: one per SIMD however the waves are placed
-        fat_producer<CB, K>(p, ft, lds, nsteps);
+        fat_producer<CB, K>(p, ft, lds, nsteps, helped);
         return;
     }
     // consumers: the wave's 16-row fragments holding rows (at most 8 in its
     // row half), rounded up to 1, 2, 4, 6 or 8 (wave-uniform)
     const int c = w / 3 * 2 + w % 3 - 1;  // 0..7
+    if (helped && c >= 4) {
+        fat_helper<CB, K>(p, ft, lds, nsteps, (c - 4) * 64 + (int)(threadIdx.x & 63));
+        return;
+    }
     const int nfr = min(8, max(0, ((ft.rows_valid + 15) >> 4) - 8 * ((c >> 2) & 1)));
     const bool mma_on = nfr > 0 && 64 * (c & 3) < p.N - ft.nt * kTN;  // a last tile may be narrower
     if (nfr <= 1)
@@ -880,7 +950,14 @@ void launch_fat_set(int cb, const FatParams& p, hipStream_t st) {
 
 // The GEMM of one launch: the K 2..4 kernel, then, when the launch reads
 // per-expert K tables, the kernel for the other K values.
-hipError_t launch_fat(int cb, const FatParams& p, hipStream_t st) {
+inline bool fat_helpers_allowed() {
+    const char* v = std::getenv("EXL3_FAT_HELPERS");
+    return !(v && std::strcmp(v, "0") == 0);
+}
+
+hipError_t launch_fat(int cb, const FatParams& p_in, hipStream_t st) {
+    FatParams p = p_in;
+    p.helpers = fat_helpers_allowed() ? 1 : 0;
     launch_fat_set<0>(cb, p, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
