@@ -105,3 +105,35 @@ def test_prefill_config2_full_size(gpu):
     dense = dense_gpu(experts, 1, gpu)
     want = torch_moe_reference(x.float(), ids, w, dense, E)
     assert rel_l2(got, want) <= TOL
+
+
+@pytest.mark.parametrize("E,T,topk", [(128, 512, 8), (1000, 300, 8), (64, 3000, 6)])
+def test_prefill_wide_router_bit_exact(gpu, monkeypatch, E, T, topk):
+    """From 2048 routes the prefill routes with the multi-workgroup router
+    (ranks per 1024-route workgroup, one scan, placement); EXL3_ROUTE_WIDE=0
+    keeps the single-workgroup router.  Same stable order, so the outputs
+    agree bit for bit; dropped ids and padded rows included.  E experts share four
+    packs (pointer tables with repeated entries), so the reference needs
+    four dequantisations."""
+    H, I = 256, 256
+    packs = S.moe_layer(700 + E, 4, H, I, 3)
+    experts = [packs[e % 4] for e in range(E)]
+    x = S.activations(701, T, H)
+    ids, w = S.softmax_topk(702 + T, T, E, topk)
+    ids[0, 0] = -1
+    ids[1, 1] = E + 5
+    n_live = T - 7
+    dl = S.to_device(experts, gpu)
+    args = (torch.from_numpy(x).to(gpu).bfloat16(), torch.from_numpy(ids).to(gpu),
+            torch.from_numpy(w).to(gpu), dl, E, I)
+    n_valid = torch.tensor([n_live], dtype=torch.int32, device=gpu)
+    outs = []
+    for wide in ("1", "0"):
+        monkeypatch.setenv("EXL3_ROUTE_WIDE", wide)
+        outs.append(C.moe_prefill(*args, K=(3, 3, 3), codebook=1, n_valid=n_valid))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.count_nonzero(outs[0][n_live:]) == 0
+    dense = dense_cpu(packs, 1)
+    want = O.moe_reference(x[:n_live], ids[:n_live], w[:n_live], [dense[e % 4] for e in range(E)])
+    assert rel_l2(outs[0][:n_live], want) <= TOL

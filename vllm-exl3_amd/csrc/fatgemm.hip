@@ -970,8 +970,16 @@ hipError_t launch_fat(int cb, const FatParams& p_in, hipStream_t st) {
 
 struct PrefillPlan {
     int n_routes, max_slots, max_mtiles;
-    size_t off_route, off_agu, off_ygu, total;
+    bool wide_route;  // the multi-workgroup router (large route counts)
+    size_t off_route, off_rscr, off_agu, off_ygu, total;
 };
+
+// EXL3_ROUTE_WIDE=0 keeps the single-workgroup router for every route count
+// (tuning and tests; read on every plan, workspace queries included).
+inline bool route_wide_allowed() {
+    const char* v = std::getenv("EXL3_ROUTE_WIDE");
+    return !(v && std::strcmp(v, "0") == 0);
+}
 
 PrefillPlan plan_prefill(int64_t T, int64_t topk, int64_t n_local, int64_t H, int64_t I, int gateless) {
     PrefillPlan pp;
@@ -979,10 +987,14 @@ PrefillPlan plan_prefill(int64_t T, int64_t topk, int64_t n_local, int64_t H, in
     pp.max_slots = (int)std::min<int64_t>(pp.n_routes, n_local);
     pp.max_mtiles = (int)route_max_mtiles(pp.n_routes, pp.max_slots, kTM);
     const int nproj = gateless ? 1 : 2;
+    pp.wide_route = route_wide_allowed() && pp.n_routes >= kRouteWideMin && pp.n_routes <= kRouteWideMax &&
+                    n_local <= kRouteMaxLocal;
     size_t off = 0;
     pp.off_route = off;
     off += a256(sizeof(int) * (3 + 3 * (size_t)pp.max_slots + 3 * (size_t)pp.n_routes +
                                2 * (size_t)pp.max_mtiles));
+    pp.off_rscr = off;  // the wide router's counts per 1024-route workgroup
+    if (pp.wide_route) off += a256(route_scratch_bytes(pp.n_routes, (int)n_local));
     pp.off_agu = off;  // A_g, A_u [n_routes][H] fp16; later Y_d [n_routes][H] fp16
     off += a256(2 * (size_t)nproj * pp.n_routes * H);
     pp.off_ygu = off;  // Y_g, Y_u [n_routes][I] fp16; A_d over Y_g
@@ -1194,7 +1206,11 @@ EXL3_API int exl3_moe_prefill(const void* x, int x_dtype, int64_t T, int64_t hid
     ro.mt_slot = ro.route_pos + pp.n_routes;
     ro.mt_row0 = ro.mt_slot + pp.max_mtiles;
     ro.n_sorted = n_sorted;
-    EXL3_HIP(launch_route(ids, ids_dtype, pp.n_routes, (int)topk, (int)n_local, n_valid, kTM, ro, st));
+    if (pp.wide_route)
+        EXL3_HIP(launch_route_wide(ids, ids_dtype, pp.n_routes, (int)topk, (int)n_local, n_valid, kTM, ro,
+                                   reinterpret_cast<int*>(ws + pp.off_rscr), st));
+    else
+        EXL3_HIP(launch_route(ids, ids_dtype, pp.n_routes, (int)topk, (int)n_local, n_valid, kTM, ro, st));
 
     uint16_t* a_g = reinterpret_cast<uint16_t*>(ws + pp.off_agu);
     uint16_t* a_u = a_g + (size_t)(nproj - 1) * pp.n_routes * hidden;

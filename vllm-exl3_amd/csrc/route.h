@@ -38,4 +38,16 @@ size_t route_lds_bytes(int n_local);
 hipError_t launch_route(const void* ids, int ids_i64, int n_routes, int topk, int n_local,
                         const int32_t* n_valid, int tile_rows, const RouteOut& o, hipStream_t st);
 
+// The same sort spread over many workgroups, for large route counts (the
+// single-workgroup sort walks n_routes / 16 routes per wave): three launches
+// (ranks and counts per 1024-route workgroup, one scan over (expert,
+// workgroup), placement) with the same outputs bit for bit.  `scratch` holds route_scratch_bytes(n_routes,
+// n_local) bytes; n_routes <= kRouteWideMax.
+constexpr int kRouteWideMin = 2048;
+constexpr int kRouteWideMax = 1 << 16;
+size_t route_scratch_bytes(int n_routes, int n_local);
+hipError_t launch_route_wide(const void* ids, int ids_i64, int n_routes, int topk, int n_local,
+                             const int32_t* n_valid, int tile_rows, const RouteOut& o, int* scratch,
+                             hipStream_t st);
+
 }  // namespace exl3
