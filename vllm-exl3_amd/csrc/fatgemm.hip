@@ -256,8 +256,30 @@ constexpr int kRowSpan = 4 * kRowGroups;  // 128-blocks per wave
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Sign of the lane's outputs of had128_x8: (-1)^popcount(lane % 16), as a
+// float and as the xor mask of a packed fp16 pair.
+__device__ __forceinline__ float had_sign(int lane) { return (__builtin_popcount(lane & 15) & 1) ? -1.0f : 1.0f; }
+__device__ __forceinline__ uint32_t had_flip(int lane) {
+    return (__builtin_popcount(lane & 15) & 1) ? 0x80008000u : 0u;
+}
+
 // 128-point butterfly (unnormalised, natural order) over the block held by
-// the lane's 16-lane group: element 8 * (lane % 16) + i is v[i].
+// the lane's 16-lane group: element 8 * (lane % 16) + i is v[i].  A
+// cross-lane stage is one v_fmac_f32_dpp per value, w + c * partner with the
+// partner's value read through a DPP row shuffle (xor 4 takes a quad_perm
+// move first) and c = +1 / -1 on the lanes whose stage bit is clear / set:
+// the butterfly's sum, or its difference with the operands swapped
+// (x_i - x_j for x_j - x_i: the same rounding, mirrored).  The partner of a
+// stage agrees with the lane in every bit already processed, so both carry
+// the same sign, and the outputs come out multiplied by had_sign(lane); the
+// callers fold that sign into a scale or an operand, exactly.
+// Wait states: a DPP read of a VGPR needs two after the VALU write of it
+// (five after an EXEC write), hence the s_nop 4 ahead of the first stage;
+// inside the sequence every DPP read is at least seven instructions after
+// the write it depends on (the eight values of a stage in turn, the xor-4
+// moves all before their multiply-adds).
+#define EXL3_FMAC_DPP(w, t, c, ctl) asm volatile("v_fmac_f32_dpp %0, %1, %2 " ctl " row_mask:0xf bank_mask:0xf" \
+                                                 : "+v"(w) : "v"(t), "v"(c))
 __device__ __forceinline__ void had128_x8(float v[8], int lane) {
 #pragma unroll
     for (int b = 1; b < 8; b <<= 1) {
@@ -269,23 +291,33 @@ __device__ __forceinline__ void had128_x8(float v[8], int lane) {
             v[i | b] = a - c;
         }
     }
+    const float c1 = (lane & 1) ? -1.0f : 1.0f, c2 = (lane & 2) ? -1.0f : 1.0f;
+    const float c4 = (lane & 4) ? -1.0f : 1.0f, c8 = (lane & 8) ? -1.0f : 1.0f;
+    float t[8];
+    asm volatile("s_nop 4" ::);
 #pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
+    for (int i = 0; i < 8; ++i) EXL3_FMAC_DPP(v[i], v[i], c1, "quad_perm:[1,0,3,2]");
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float p = __shfl_xor(v[i], m, 64);
-            v[i] = (lane & m) ? p - v[i] : v[i] + p;
-        }
-    }
+    for (int i = 0; i < 8; ++i) EXL3_FMAC_DPP(v[i], v[i], c2, "quad_perm:[2,3,0,1]");
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        asm volatile("v_mov_b32_dpp %0, %1 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf" : "=v"(t[i]) : "v"(v[i]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) EXL3_FMAC_DPP(v[i], t[i], c4, "row_half_mirror");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) EXL3_FMAC_DPP(v[i], v[i], c8, "row_ror:8");
 }
+#undef EXL3_FMAC_DPP
 
-// Elements i..i+7 (i % 8 == 0) of an fp16 array.
-__device__ __forceinline__ void ld_f16x8(const uint16_t* p, int64_t i, float v[8]) {
+// Elements i..i+7 (i % 8 == 0) of an fp16 array; `flip` (0 or 0x80008000)
+// negates them.
+__device__ __forceinline__ void ld_f16x8(const uint16_t* p, int64_t i, float v[8], uint32_t flip = 0) {
     const u32x4_t w = *reinterpret_cast<const u32x4_t*>(p + i);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        v[2 * k] = (float)bits_to_half(w[k] & 0xFFFFu);
-        v[2 * k + 1] = (float)bits_to_half(w[k] >> 16);
+        const uint32_t x = w[k] ^ flip;
+        v[2 * k] = (float)bits_to_half(x & 0xFFFFu);
+        v[2 * k + 1] = (float)bits_to_half(x >> 16);
     }
 }
 
@@ -391,6 +423,7 @@ __global__ __launch_bounds__(256) void rotate_in_kernel(const void* x, int x_dty
 #pragma unroll
         for (int g = 0; g < kRowGroups; ++g) ld_f16x8(su[q], rc.col[g], sv[q][g]);
     }
+    const float scale = kHadNorm * had_sign(lane);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         if (q >= nproj) break;
@@ -401,7 +434,7 @@ __global__ __launch_bounds__(256) void rotate_in_kernel(const void* x, int x_dty
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = xv[g][i] * sv[q][g][i];
             had128_x8(v, lane);
-            if (rc.ok[g]) st_f16x8(dst, rc.col[g], v, kHadNorm);
+            if (rc.ok[g]) st_f16x8(dst, rc.col[g], v, scale);
         }
     }
 }
@@ -445,15 +478,18 @@ __global__ __launch_bounds__(256) void act_kernel(const int* n_sorted, const int
     const uint16_t* svg = reinterpret_cast<const uint16_t*>(svh_g[e]);
     const uint16_t* sud = reinterpret_cast<const uint16_t*>(suh_d[e]);
     const int64_t ro = (int64_t)row * I;
+    // the output scales carry had128_x8's lane sign
+    const uint32_t flip = had_flip(lane);
+    const float scale = kHadNorm * had_sign(lane);
     float u[kRowGroups][8], g[kRowGroups][8], vu[kRowGroups][8], vg[kRowGroups][8], d[kRowGroups][8];
 #pragma unroll
     for (int q = 0; q < kRowGroups; ++q) {
         ld_f16x8(y_u, ro + rc.col[q], u[q]);
-        ld_f16x8(svu, rc.col[q], vu[q]);
+        ld_f16x8(svu, rc.col[q], vu[q], flip);
         ld_f16x8(sud, rc.col[q], d[q]);
         if (!gateless) {
             ld_f16x8(y_g, ro + rc.col[q], g[q]);
-            ld_f16x8(svg, rc.col[q], vg[q]);
+            ld_f16x8(svg, rc.col[q], vg[q], flip);
         }
     }
 #pragma unroll
@@ -468,7 +504,7 @@ __global__ __launch_bounds__(256) void act_kernel(const int* n_sorted, const int
             r[i] = (float)f32_to_f16_rne(activate(gg, uu, act, limit)) * d[q][i];
         }
         had128_x8(r, lane);
-        if (rc.ok[q]) st_f16x8(y_g, ro + rc.col[q], r, kHadNorm);
+        if (rc.ok[q]) st_f16x8(y_g, ro + rc.col[q], r, scale);
     }
 }
 
@@ -504,6 +540,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_
             w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wi]);
         else
             w = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wi] << 16);
+        w *= had_sign(lane);  // had128_x8's lane sign
         float v[kRowGroups][8], h[kRowGroups][8];
 #pragma unroll
         for (int q = 0; q < kRowGroups; ++q) {
@@ -575,7 +612,7 @@ __global__ __launch_bounds__(256) void linear_rotate_kernel(const void* x, int x
 #pragma unroll
         for (int i = 0; i < 8; ++i) xv[g][i] *= sv[g][i];
         had128_x8(xv[g], lane);
-        if (rc.ok[g]) st_f16x8(a, row * H + rc.col[g], xv[g], kHadNorm);
+        if (rc.ok[g]) st_f16x8(a, row * H + rc.col[g], xv[g], kHadNorm * had_sign(lane));
     }
 }
 
@@ -601,7 +638,7 @@ __global__ __launch_bounds__(256) void linear_out_kernel(const float* z, int N, 
             v[g][k] = a[k];
             v[g][4 + k] = b[k];
         }
-        ld_f16x8(svh, rc.col[g], h[g]);
+        ld_f16x8(svh, rc.col[g], h[g], had_flip(lane));  // with had128_x8's lane sign
     }
 #pragma unroll
     for (int g = 0; g < kRowGroups; ++g) {
