@@ -885,17 +885,24 @@ __device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     // at most 128 rows: the second row half's MFMA waves help decode B
     const bool helped = ft.rows_valid <= 128 && fat_helpers_on(p);
-    if (w % 3 == 0) {  // waves 0, 3, 6, 9: one per SIMD however the waves are placed
+    if (w % 3 == 0) {  // waves 0, 3, 6, 9: one per SIMD
         fat_producer<CB, K>(p, ft, lds, nsteps, helped);
         return;
     }
-    // consumers: the wave's 16-row fragments holding rows (at most 8 in its
-    // row half), rounded up to 1, 2, 4, 6 or 8 (wave-uniform)
-    const int c = w / 3 * 2 + w % 3 - 1;  // 0..7
+    // consumers: c = 0..3 row half 0, 4..7 row half 1 (the helpers of a tile
+    // of at most 128 rows).  The dispatcher puts waves w, w + 4 and w + 8 on
+    // one SIMD (measured: the SIMD of wave w is a fixed permutation of w % 4,
+    // rotated per workgroup), so each SIMD holds one producer (0, 3, 6, 9),
+    // one half-0 wave (1, 2, 4, 7) and one half-1 wave (5, 8, 10, 11): the
+    // decode and the MFMAs spread evenly whatever the tile's row count.
+    // Nibble w of the constant is c (F: producer).
+    const int c = (int)((0x76F53F42F10Full >> (4 * w)) & 15);
     if (helped && c >= 4) {
         fat_helper<CB, K>(p, ft, lds, nsteps, (c - 4) * 64 + (int)(threadIdx.x & 63));
         return;
     }
+    // the wave's 16-row fragments holding rows (at most 8 in its row half),
+    // rounded up to 1, 2, 4, 6 or 8 (wave-uniform)
     const int nfr = min(8, max(0, ((ft.rows_valid + 15) >> 4) - 8 * ((c >> 2) & 1)));
     const bool mma_on = nfr > 0 && 64 * (c & 3) < p.N - ft.nt * kTN;  // a last tile may be narrower
     if (nfr <= 1)
