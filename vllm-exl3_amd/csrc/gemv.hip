@@ -228,8 +228,9 @@ __device__ __forceinline__ void sum_splits(const float* __restrict__ base, int64
 __device__ __forceinline__ void finish_block(float& v0, float& v1, const uint16_t* svh, int c0,
                                              int lane) {
     had128(v0, v1, lane);
-    v0 = v0 * kHadNorm * (float)bits_to_half(svh[c0]);
-    v1 = v1 * kHadNorm * (float)bits_to_half(svh[c0 + 64]);
+    const float hs = kHadNorm * had_sign64(lane);  // with had128's lane sign
+    v0 = v0 * hs * (float)bits_to_half(svh[c0]);
+    v1 = v1 * hs * (float)bits_to_half(svh[c0 + 64]);
 }
 
 // The activation of one route row and 128-block hb of the intermediate
@@ -254,8 +255,9 @@ __device__ __forceinline__ void act_finish(float (&v)[2][2], const Proj* gu, int
     a[0] *= (float)bits_to_half(down_suh[c0]);
     a[1] *= (float)bits_to_half(down_suh[c0 + 64]);
     had128(a[0], a[1], lane);
-    a0 = a[0] * kHadNorm;
-    a1 = a[1] * kHadNorm;
+    const float hs = kHadNorm * had_sign64(lane);  // with had128's lane sign
+    a0 = a[0] * hs;
+    a1 = a[1] * hs;
 }
 
 // Finish gate/up for one route row and 128-block hb from the split partials.
@@ -334,9 +336,10 @@ __global__ __launch_bounds__(256) void rotate_rows_kernel(RotateArgs a) {
         float v0 = x0 * (float)bits_to_half(su[fb + lane]);
         float v1 = x1 * (float)bits_to_half(su[fb + lane + 64]);
         had128(v0, v1, lane);
+        const float hs = kHadNorm * had_sign64(lane);  // with had128's lane sign
         uint16_t* dst = a.img[q] + row * a.in_f;
-        dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0 * kHadNorm));
-        dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1 * kHadNorm));
+        dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0 * hs));
+        dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1 * hs));
     }
 }
 
@@ -947,9 +950,10 @@ __device__ __forceinline__ void wg_stage_rotate(const GemvParams& p, const WgGro
             const int r = u / nb, b = u - r * nb;
             float v0 = v[i][0] * su[i][0], v1 = v[i][1] * su[i][1];
             had128(v0, v1, lane);
+            const float hs = kHadNorm * had_sign64(lane);  // with had128's lane sign
             const int c0 = lane, c1 = lane + 64;
-            A[((b * 8 + (c0 >> 4)) * MRB + r) * 16 + pi_inv(c0 & 15)] = half_to_bits(f32_to_f16_rne(v0 * kHadNorm));
-            A[((b * 8 + (c1 >> 4)) * MRB + r) * 16 + pi_inv(c1 & 15)] = half_to_bits(f32_to_f16_rne(v1 * kHadNorm));
+            A[((b * 8 + (c0 >> 4)) * MRB + r) * 16 + pi_inv(c0 & 15)] = half_to_bits(f32_to_f16_rne(v0 * hs));
+            A[((b * 8 + (c1 >> 4)) * MRB + r) * 16 + pi_inv(c1 & 15)] = half_to_bits(f32_to_f16_rne(v1 * hs));
         }
     }
 }
@@ -1287,9 +1291,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_rotate_kernel(RouteRotate
             float v0 = x0 * (float)bits_to_half(su[fb + lane]);
             float v1 = x1 * (float)bits_to_half(su[fb + lane + 64]);
             had128(v0, v1, lane);
+            const float hs = kHadNorm * had_sign64(lane);  // with had128's lane sign
             uint16_t* dst = (q ? f.img1 : f.img0) + r * f.hidden;
-            dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0 * kHadNorm));
-            dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1 * kHadNorm));
+            dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0 * hs));
+            dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1 * hs));
         }
     }
 }

@@ -268,21 +268,58 @@ __device__ __forceinline__ float4_t mfma16x16x32(const half8_t& a, const uint32_
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8_t, bv), c, 0, 0, 0);
 }
 
-// Butterfly over 128 values held as (lane, lane + 64), strides 1..64.
+// Butterfly over 128 values held as (lane, lane + 64), strides 1..64.  A
+// lane stage (strides 1..32) is w + c * partner with c = -1 on the lanes
+// whose stage bit is set: the butterfly's difference with its operands
+// swapped (x_i - x_j for x_j - x_i, the same rounding mirrored).  A stage's
+// partner agrees with the lane in every bit already processed, so both carry
+// the same sign, and the outputs come out multiplied by had_sign64(lane) =
+// (-1)^popcount(lane); the callers fold that sign into their scale, exactly.
+// Strides 1, 2, 4, 8 read the partner through DPP row shuffles inside
+// v_fmac_f32_dpp (4 takes a quad_perm move first); 16 and 32 through the
+// gfx950 permlane swaps of two copies, which leave (own, partner) on the
+// lanes whose bit is clear and (partner, own) on the others, so one
+// fma(first, c, second) finishes the stage.  No LDS.  Wait states: two
+// after a VALU write before a DPP or permlane read of it (five after an EXEC
+// write), written out because inline assembly is opaque to the compiler's
+// hazard checks.
+__device__ __forceinline__ float had_sign64(int lane) { return (__builtin_popcount(lane & 63) & 1) ? -1.0f : 1.0f; }
+
 __device__ __forceinline__ void had128(float& v0, float& v1, int lane) {
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        float p0 = __shfl_xor(v0, s, 64);
-        float p1 = __shfl_xor(v1, s, 64);
-        if (lane & s) {
-            v0 = p0 - v0;
-            v1 = p1 - v1;
-        } else {
-            v0 = v0 + p0;
-            v1 = v1 + p1;
-        }
-    }
-    float a = v0, b = v1;
+    const float c1 = (lane & 1) ? -1.0f : 1.0f, c2 = (lane & 2) ? -1.0f : 1.0f;
+    const float c4 = (lane & 4) ? -1.0f : 1.0f, c8 = (lane & 8) ? -1.0f : 1.0f;
+    const float c16 = (lane & 16) ? -1.0f : 1.0f, c32 = (lane & 32) ? -1.0f : 1.0f;
+    float t0, t1;
+    asm volatile(
+        "s_nop 4\n\t"
+        "v_fmac_f32_dpp %0, %0, %4 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %1, %4 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %0, %5 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %1, %5 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_mov_b32_dpp %2, %0 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b32_dpp %3, %1 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %2, %6 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %3, %6 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %0, %7 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %1, %7 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1"
+        : "+v"(v0), "+v"(v1), "=&v"(t0), "=&v"(t1)
+        : "v"(c1), "v"(c2), "v"(c4), "v"(c8));
+    float a0 = v0, b0 = v0, a1 = v1, b1 = v1;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_permlane16_swap_b32 %2, %3\n\ts_nop 1"
+                 : "+v"(a0), "+v"(b0), "+v"(a1), "+v"(b1));
+    v0 = __builtin_fmaf(a0, c16, b0);
+    v1 = __builtin_fmaf(a1, c16, b1);
+    a0 = v0, b0 = v0, a1 = v1, b1 = v1;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\tv_permlane32_swap_b32 %2, %3\n\ts_nop 1"
+                 : "+v"(a0), "+v"(b0), "+v"(a1), "+v"(b1));
+    v0 = __builtin_fmaf(a0, c32, b0);
+    v1 = __builtin_fmaf(a1, c32, b1);
+    const float a = v0, b = v1;
     v0 = a + b;
     v1 = a - b;
 }
