@@ -698,7 +698,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 //   row_bytes: bytes between consecutive tile rows (tiles_n * 32K)
 //   nkt:       tile rows in the chunk; the wave takes rows wave, wave+4, ...
 //   A:         this projection's activations [nkt][MRB][16] fp16 (kappa order)
-// The pipeline keeps kDepth rows in flight.  Its steady state has no
+// The pipeline keeps kWgDepth rows in flight.  Its steady state has no
 // branches: lanes past the 256*K-byte row span reload the span's first 16
 // bytes, prefetches past the last row reload the last row (all in bounds),
 // and every lane stores into the 1 KB stage (bytes past the span are never
@@ -709,10 +709,10 @@ struct WgStream {
     uint32_t voff;        // this lane's 16 bytes of a row
     uint32_t step;        // bytes between the wave's consecutive rows (the scalar offset)
     int n;                // rows of this wave in the chunk
-    v4u buf[kDepth];
+    v4u buf[kWgDepth];
 };
 
-// Issue the loads of the wave's first kDepth rows (clamped, in bounds) so
+// Issue the loads of the wave's first kWgDepth rows (clamped, in bounds) so
 // they are in flight while the activations are staged.
 template <int K>
 __device__ __forceinline__ void wg_prefetch(WgStream<K>& rs, const uint8_t* tbase,
@@ -724,7 +724,7 @@ __device__ __forceinline__ void wg_prefetch(WgStream<K>& rs, const uint8_t* tbas
     rs.step = (uint32_t)(row_bytes * kWaves);  // a chunk lies within one projection (< 2 GiB)
     if (rs.n == 0) return;
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) rs.buf[d] = load_row(rs.base, rs.voff, (uint32_t)min(d, rs.n - 1) * rs.step);
+    for (int d = 0; d < kWgDepth; ++d) rs.buf[d] = load_row(rs.base, rs.voff, (uint32_t)min(d, rs.n - 1) * rs.step);
 }
 
 // Consume the wave's rows: per row, stage 256*K bytes in LDS, refill the
@@ -748,7 +748,7 @@ __device__ __forceinline__ void wg_consume(WgStream<K>& rs, int wave, int lane, 
     const int a_step = kWaves * MRB * 8;  // uint32 words between this wave's consecutive rows
     auto consume = [&](int d, int i) {
         reinterpret_cast<v4u*>(stage)[lane] = rs.buf[d];
-        rs.buf[d] = load_row(rs.base, rs.voff, (uint32_t)min(i + kDepth, n - 1) * rs.step);
+        rs.buf[d] = load_row(rs.base, rs.voff, (uint32_t)min(i + kWgDepth, n - 1) * rs.step);
         const uint32_t* ap = arow_p + (size_t)i * a_step;
         // all sixteen words of the row first: one LDS latency per row
         uint32_t wh[8], wl[8];
@@ -766,12 +766,12 @@ __device__ __forceinline__ void wg_consume(WgStream<K>& rs, int wave, int lane, 
         }
     };
     int i = 0;
-    for (; i + kDepth <= n; i += kDepth) {
+    for (; i + kWgDepth <= n; i += kWgDepth) {
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d) consume(d, i + d);
+        for (int d = 0; d < kWgDepth; ++d) consume(d, i + d);
     }
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d)
+    for (int d = 0; d < kWgDepth; ++d)
         if (i + d < n) consume(d, i + d);
 }
 

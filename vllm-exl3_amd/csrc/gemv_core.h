@@ -43,7 +43,15 @@ enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kDepth = 8;          // tile rows in flight per wave
+// Tile rows in flight per wave: kDepth in the persistent kernel, kWgDepth in
+// the one-unit kernel.  Both kernels are VALU-bound while their waves are
+// resident, so fewer rows in flight cost nothing there and shorten every
+// workgroup's cold start: at a launch's first round all workgroups request
+// their first rows at once (C1 T = 16 gate/up 58.4 -> 57.2 µs with 8 -> 4
+// and 2, T = 1 step about -2 µs at 2; C3's persistent kernel is 2% faster at
+// 4 and 8% slower at 2).
+constexpr int kDepth = 4;
+constexpr int kWgDepth = 2;
 constexpr int kStageBytes = 1024;  // one tile row of 8 tiles at K <= 4
 
 struct GemvParams {
