@@ -46,7 +46,7 @@ FP16_FLOP_PER_CLK_CU = 4096  # gfx950: 4 SIMDs x 1024 dense fp16 FLOP per clock
 # HBM bytes of one gate/up launch at T=16 (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000,
 # factors from a 256 MiB copy), from profiles/moe_decode_c1_t16.md; re-measured
 # with rocprofv3 --pmc whenever the kernel changes.
-GATE_UP_TRAFFIC_T16 = 145_330_553 + 3_145_728
+GATE_UP_TRAFFIC_T16 = 141_743_309 + 3_145_728
 
 
 def cpu_model() -> str:
