@@ -390,9 +390,11 @@ def attention_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) 
 #   [1024, 2048)  V codes: dim-major nibbles in the order the PV operand reads
 #                 them (lane l = m + 16 j for dims 16 b + m and tokens
 #                 4 j + i; word b // 2, bit 8 (b % 2) + (0, 16, 4, 20)[i]).
-#   [2048, 2176)  K scale fp16 [4 groups][16 tokens]
+#   [2048, 2176)  K scale fp16 [4 token quads][4 groups][4 tokens] (token
+#                 4 j + i at 16 j + 4 g + i: a decode lane's 16 scales, its
+#                 four tokens in every group, are 32 contiguous bytes)
 #   [2176, 2304)  K zero  fp16 [4 groups][16 tokens]
-#   [2304, 2432)  V scale fp16 [4 groups][16 tokens]
+#   [2304, 2432)  V scale fp16 [4 token quads][4 groups][4 tokens]
 #   [2432, 2560)  V zero  fp16 [4 groups][16 tokens]
 # The pool is uint8 [num_pages, num_kv_heads, 2560]; a sequence's logical
 # page i lives at physical page block_table[b, i].
@@ -462,9 +464,19 @@ def kv_pack_pages(k: np.ndarray, v: np.ndarray, seq_lens: np.ndarray, block_tabl
                     s[cnt:] = 0
                     z[cnt:] = 0
                     _put_nibbles(page, bits, q)
-                    page[off_s:off_s + 128] = np.ascontiguousarray(s.T).view(np.uint8).ravel()
+                    page[off_s:off_s + 128] = _scales_to_page(s).view(np.uint8).ravel()
                     page[off_z:off_z + 128] = np.ascontiguousarray(z.T).view(np.uint8).ravel()
     return pool
+
+
+def _scales_to_page(s: np.ndarray) -> np.ndarray:
+    """Scales [16 tokens, 4 groups] in page order [token quad][group][token % 4]."""
+    return np.ascontiguousarray(s.reshape(4, 4, 4).transpose(0, 2, 1)).ravel()
+
+
+def _scales_from_page(w: np.ndarray) -> np.ndarray:
+    """Inverse of _scales_to_page: [16 tokens, 4 groups]."""
+    return np.ascontiguousarray(w.reshape(4, 4, 4).transpose(0, 2, 1)).reshape(KV_PAGE, 4)
 
 
 def kv_unpack_page(page: np.ndarray, side: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
@@ -473,7 +485,7 @@ def kv_unpack_page(page: np.ndarray, side: int) -> tuple[np.ndarray, np.ndarray,
     bits = kv_k_nibble_bit(tt, dd) if side == 0 else kv_v_nibble_bit(tt, dd)
     q = _get_nibbles(np.asarray(page, dtype=np.uint8), bits).astype(np.uint8)
     off_s, off_z = (KV_OFF_KS, KV_OFF_KZ) if side == 0 else (KV_OFF_VS, KV_OFF_VZ)
-    s = np.ascontiguousarray(page[off_s:off_s + 128]).view(np.float16).reshape(4, KV_PAGE).T
+    s = _scales_from_page(np.ascontiguousarray(page[off_s:off_s + 128]).view(np.float16))
     z = np.ascontiguousarray(page[off_z:off_z + 128]).view(np.float16).reshape(4, KV_PAGE).T
     return q, s, z
 

@@ -8,9 +8,14 @@
 // 16-token pages.  A page of one KV head is 2560 bytes:
 //   [   0, 1024)  K codes, token-major, in QK matrix-core operand order
 //   [1024, 2048)  V codes, dim-major, in PV matrix-core operand order
-//   [2048, 2560)  K scale, K zero, V scale, V zero: fp16 [4 groups][16 tokens]
+//   [2048, 2560)  K scale, K zero, V scale, V zero (128 B each): the zeros
+//                 fp16 [4 groups][16 tokens], the scales fp16 [4 token
+//                 quads][4 groups][4 tokens]
 // so that every lane of a decode wave fetches its K and V codes of a page
-// with one 16-byte load each and feeds them to MFMA without any shuffle.
+// with one 16-byte load each and feeds them to MFMA without any shuffle, and
+// its tokens' scales with two 16-byte loads per side (nine loads per page;
+// the load count, not the bytes, bounded this kernel: scales as [group]
+// [token], eight 8-byte loads, took 171 µs on C4 against 131-143 µs).
 //
 // Decode (one wave per (sequence, KV head, split of the pages)):
 //   QK   S^T[t][h] = sum_g s[t,g] * D_g[t][h] + corr[t][h], where D_g is one
@@ -83,6 +88,12 @@ __device__ __forceinline__ int v_code_bit(int t, int d) {
     const int ib = (i == 0) ? 0 : (i == 1) ? 16 : (i == 2) ? 4 : 20;
     return (kOffVQ + 16 * (m + 16 * j) + 4 * (b >> 1)) * 8 + 8 * (b & 1) + ib;
 }
+
+// Index (fp16 element) of the scale of token t, group g inside a page's scale
+// array: [token quad][group][token % 4], so that a decode lane's 16 scales
+// (its four tokens in every group) are 32 contiguous bytes, two 16-byte
+// loads.  Zeros keep [group][token].
+__device__ __forceinline__ int kv_scale_index(int t, int g) { return 16 * (t >> 2) + 4 * g + (t & 3); }
 
 // ---------------------------------------------------------------------------
 // Pack: one wave per (sequence, logical page, KV head).
@@ -182,7 +193,7 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(KvPackParams p) {
             const int offs = side ? kOffVS : kOffKS, offz = side ? kOffVZ : kOffKZ;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                *reinterpret_cast<uint16_t*>(base + offs + 2 * (16 * g + t)) = s16[g];
+                *reinterpret_cast<uint16_t*>(base + offs + 2 * kv_scale_index(t, g)) = s16[g];
                 *reinterpret_cast<uint16_t*>(base + offz + 2 * (16 * g + t)) = z16[g];
             }
         }
@@ -239,7 +250,7 @@ __global__ __launch_bounds__(256) void kv_unpack_kernel(const uint8_t* pool, int
         const int bit = side ? v_code_bit(t, d) : k_code_bit(t, d);
         const uint32_t c = (base[bit >> 3] >> (bit & 7)) & 0xFu;
         const int gi = 16 * (d >> 5) + t;
-        const float s = (float)bits_to_half(sc[(side ? 128 : 0) + gi]);
+        const float s = (float)bits_to_half(sc[(side ? 128 : 0) + kv_scale_index(t, d >> 5)]);
         const float z = (float)bits_to_half(sc[(side ? 192 : 64) + gi]);
         float* o = side ? v_out : k_out;
         o[(((int64_t)b * Hkv + h) * L + pos) * kKvDim + d] = (float)c * s + z;
@@ -281,8 +292,9 @@ struct PageRegs {
 // Per-lane byte offsets inside a page (constant over the page loop).
 struct PageOffsets {
     int codes;  // 16 lane: K codes at +0, V codes at +1024
-    int scl;    // 8 j: K scales at +2048 + 32 g, V scales at +2304 + 32 g
-    int kzs;    // 32 j + 2 n: K zero at +2176, K scale at +2048
+    int scl;    // 32 j: the lane's tokens' K scales at +2048, V scales at +2304 (32 B each)
+    int kzs;    // 32 j + 2 n: K zero of (group j, token n) at +2176
+    int ksn;    // K scale of (group j, token n) at +2048
     int vz;     // 32 min(n, 3) + 8 j: V zeros at +2432
 };
 
@@ -293,14 +305,24 @@ __device__ __forceinline__ void load_page(PageRegs& r, const uint8_t* base, cons
         __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, kKvPageBytes, 0x00020000);
     r.kq = __builtin_amdgcn_raw_buffer_load_b128(rs, o.codes, 0, 0);
     r.vq = __builtin_amdgcn_raw_buffer_load_b128(rs, o.codes + kOffVQ, 0, 0);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        r.ks[g] = __builtin_amdgcn_raw_buffer_load_b64(rs, o.scl + kOffKS + 32 * g, 0, 0);
-        r.vs[g] = __builtin_amdgcn_raw_buffer_load_b64(rs, o.scl + kOffVS + 32 * g, 0, 0);
+    {
+        // the lane's four tokens in all four groups: 32 contiguous bytes per side
+        const u32x4 k0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, o.scl + kOffKS, 0, 0));
+        const u32x4 k1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, o.scl + kOffKS + 16, 0, 0));
+        const u32x4 v0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, o.scl + kOffVS, 0, 0));
+        const u32x4 v1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, o.scl + kOffVS + 16, 0, 0));
+        r.ks[0] = u32x2{k0.x, k0.y};
+        r.ks[1] = u32x2{k0.z, k0.w};
+        r.ks[2] = u32x2{k1.x, k1.y};
+        r.ks[3] = u32x2{k1.z, k1.w};
+        r.vs[0] = u32x2{v0.x, v0.y};
+        r.vs[1] = u32x2{v0.z, v0.w};
+        r.vs[2] = u32x2{v1.x, v1.y};
+        r.vs[3] = u32x2{v1.z, v1.w};
     }
     // kept apart until use: combining them here would wait on the loads
     r.zk = __builtin_amdgcn_raw_buffer_load_b16(rs, o.kzs + kOffKZ, 0, 0);
-    r.sk = __builtin_amdgcn_raw_buffer_load_b16(rs, o.kzs + kOffKS, 0, 0);
+    r.sk = __builtin_amdgcn_raw_buffer_load_b16(rs, o.ksn + kOffKS, 0, 0);
     r.vz = __builtin_amdgcn_raw_buffer_load_b64(rs, o.vz + kOffVZ, 0, 0);
 }
 
@@ -443,8 +465,9 @@ __global__ __launch_bounds__(64 * kKvWaves, 2) void kv_decode_kernel(KvDecodePar
     const uint8_t* hbase = p.pool + (int64_t)h * kKvPageBytes;
     PageOffsets offs;
     offs.codes = 16 * lane;
-    offs.scl = 8 * j;
+    offs.scl = 32 * j;
     offs.kzs = 32 * j + 2 * n;
+    offs.ksn = 2 * kv_scale_index(n, j);
     offs.vz = 32 * min(n, 3) + 8 * j;
 
     // QK^T of one page, the scale fold and the zero/offset correction; with
