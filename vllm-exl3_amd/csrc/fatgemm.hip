@@ -677,6 +677,36 @@ __device__ __forceinline__ void decode_group_half(const uint32_t (&w)[K + 1], ui
     }
 }
 
+// The K + 1 packed words a thread decodes: the K words of its group (word
+// offsets g K .. g K + K - 1 of the tile, contiguous) in one wide load, and
+// the word before (the tile's last word for group 0, where the bitstream
+// wraps) in one more.  Per k-step the load count, not the bytes, weighs on
+// few-row tiles: K + 1 four-byte loads made 32 x 4096 x 65536 take 103 µs,
+// these two (three for K 5, 6) 85 µs.
+template <int K>
+__device__ __forceinline__ void load_group_words(uint32_t (&w)[K + 1], __amdgpu_buffer_rsrc_t trs, int wprev,
+                                                 int wfirst, int soff) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(trs, wprev, soff, 0);
+    if constexpr (K == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(trs, wfirst, soff, 0);
+        w[1] = v[0];
+        w[2] = v[1];
+    } else if constexpr (K == 3) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b96(trs, wfirst, soff, 0);
+        w[1] = v[0];
+        w[2] = v[1];
+        w[3] = v[2];
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(trs, wfirst, soff, 0);
+        w[1] = v[0];
+        w[2] = v[1];
+        w[3] = v[2];
+        w[4] = v[3];
+        if constexpr (K >= 5) w[5] = __builtin_amdgcn_raw_buffer_load_b32(trs, wfirst + 16, soff, 0);
+        if constexpr (K >= 6) w[6] = __builtin_amdgcn_raw_buffer_load_b32(trs, wfirst + 20, soff, 0);
+    }
+}
+
 // Producer waves (0..3, one per SIMD): global loads of A rows and packed
 // bits two k-steps ahead of their staging; per k-step each thread stages 64
 // bytes of A and decodes one 32-weight group (both column halves) into the
@@ -701,12 +731,10 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
         (void*)(ft.trellis + (size_t)ft.nt * 16 * tile_bytes), (short)0, 0x7FFFFFFF, 0x00020000);
     const int t_voff = (tr * tiles_n + min(tc, tcols - 1)) * tile_bytes;
     const int step_bytes = 2 * tiles_n * tile_bytes;
-    int w_voff[K + 1];
-#pragma unroll
-    for (int j = 0; j < K + 1; ++j) {
-        const int idx = g * K - 1 + j;
-        w_voff[j] = t_voff + 4 * (idx < 0 ? idx + 8 * K : idx);
-    }
+    // the group's first word, and the word before it (wrapping to the
+    // tile's last word for group 0)
+    const int w_first = t_voff + 4 * g * K;
+    const int w_prev = t_voff + 4 * (g == 0 ? 8 * K - 1 : g * K - 1);
     const int col0 = tc * 16 + g;
 
     v4u ga[2][4];
@@ -716,9 +744,7 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj)
             ga[r][jj] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff[jj], so * (kTK * 2), 0));
-#pragma unroll
-        for (int j = 0; j < K + 1; ++j)
-            gw[r][j] = __builtin_amdgcn_raw_buffer_load_b32(trs, w_voff[j], so * step_bytes, 0);
+        load_group_words<K>(gw[r], trs, w_prev, w_first, so * step_bytes);
     };
     auto stage = [&](int st, int r) {
         uint8_t* A = lds + st * kABytes;
@@ -769,19 +795,15 @@ __device__ __forceinline__ void fat_helper(const FatParams& p, const FatTile& ft
         (void*)(ft.trellis + (size_t)ft.nt * 16 * tile_bytes), (short)0, 0x7FFFFFFF, 0x00020000);
     const int t_voff = (tr * tiles_n + min(tc, tcols - 1)) * tile_bytes;
     const int step_bytes = 2 * tiles_n * tile_bytes;
-    int w_voff[K + 1];
-#pragma unroll
-    for (int j = 0; j < K + 1; ++j) {
-        const int idx = g * K - 1 + j;
-        w_voff[j] = t_voff + 4 * (idx < 0 ? idx + 8 * K : idx);
-    }
+    // the group's first word, and the word before it (wrapping to the
+    // tile's last word for group 0)
+    const int w_first = t_voff + 4 * g * K;
+    const int w_prev = t_voff + 4 * (g == 0 ? 8 * K - 1 : g * K - 1);
     const int col0 = tc * 16 + g;
     uint32_t gw[2][K + 1];
     auto load = [&](int t, int r) {
         const int so = min(t, nsteps - 1);
-#pragma unroll
-        for (int j = 0; j < K + 1; ++j)
-            gw[r][j] = __builtin_amdgcn_raw_buffer_load_b32(trs, w_voff[j], so * step_bytes, 0);
+        load_group_words<K>(gw[r], trs, w_prev, w_first, so * step_bytes);
     };
     auto stage = [&](int st, int r) {
         uint8_t* B = lds + kStages * kABytes + st * kBBytes;
