@@ -444,14 +444,15 @@ __device__ __forceinline__ void q4_load_piece(const uint8_t* base, int tid, Q4Pi
     pc.k1 = ksrc[1];
     pc.v0 = vsrc[0];
     pc.v1 = vsrc[1];
-    uint32_t ks = 0, vs = 0;
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-        ks |= (uint32_t)base[kQ4Data + scale_offset(0, t, 4 * h + gi)] << (8 * gi);
-        vs |= (uint32_t)base[kQ4Slot + kQ4Data + scale_offset(1, t, 4 * h + gi)] << (8 * gi);
-    }
-    pc.ks = ks;
-    pc.vs = vs;
+    // scale bytes of groups 4h .. 4h + 3 (scale_offset): K's are four
+    // consecutive bytes; V's are byte t % 4 of four consecutive words of one
+    // 16-byte block (two loads in place of eight byte loads; the same time,
+    // 41 µs on the bench's workload)
+    pc.ks = *reinterpret_cast<const uint32_t*>(base + kQ4Data + t * 8 + 4 * h);
+    const u32x4 vw = *reinterpret_cast<const u32x4*>(base + kQ4Slot + kQ4Data + (t >> 2) * 32 + 16 * h);
+    const uint32_t q = (uint32_t)(t & 3);
+    const uint32_t sel = q | ((q + 4) << 8) | 0x0C0C0000u;  // bytes (lo.q, hi.q, 0, 0)
+    pc.vs = __builtin_amdgcn_perm(vw.y, vw.x, sel) | (__builtin_amdgcn_perm(vw.w, vw.z, sel) << 16);
 }
 
 // The eight fp16 values of one packed word (dims 2b, 2b + 1 in byte b, low
