@@ -711,7 +711,7 @@ __device__ __forceinline__ void load_group_words(uint32_t (&w)[K + 1], __amdgpu_
 // bits two k-steps ahead of their staging; per k-step each thread stages 64
 // bytes of A and decodes one 32-weight group (both column halves) into the
 // B stage.  One barrier per k-step, three stages, as the consumers.
-template <int CB, int K>
+template <int CB, int K, int NA>
 __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& ft, uint8_t* lds, int nsteps,
                                              bool helped) {
     constexpr int tile_bytes = 32 * K;
@@ -720,9 +720,13 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
     const int ac = pt & 3, ar0 = pt >> 2;  // A: chunk ac of rows ar0 + 64 jj
     const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.a + ft.a_row0 * p.lda), (short)0, 0x7FFFFFFF, 0x00020000);
-    int a_voff[4];
+    // NA of the four 64-row groups of A hold the tile's rows (a compile-time
+    // count, so every load is unconditional and the wait counts exact): the
+    // others are neither loaded nor staged, the MFMA rows they would feed
+    // are never read
+    int a_voff[NA];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
+    for (int jj = 0; jj < NA; ++jj)
         a_voff[jj] = (int)((min(ar0 + 64 * jj, ft.rows_valid - 1) * p.lda + 8 * ac) * 2);
     const int t_idx = pt >> 3, g = pt & 7;  // decode: group g of tile t_idx
     const int tr = t_idx >> 4, tc = t_idx & 15;
@@ -737,12 +741,12 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
     const int w_prev = t_voff + 4 * (g == 0 ? 8 * K - 1 : g * K - 1);
     const int col0 = tc * 16 + g;
 
-    v4u ga[2][4];
+    v4u ga[2][NA];
     uint32_t gw[2][K + 1];
     auto load = [&](int t, int r) {
         const int so = min(t, nsteps - 1);
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
+        for (int jj = 0; jj < NA; ++jj)
             ga[r][jj] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff[jj], so * (kTK * 2), 0));
         load_group_words<K>(gw[r], trs, w_prev, w_first, so * step_bytes);
     };
@@ -750,7 +754,7 @@ __device__ __forceinline__ void fat_producer(const FatParams& p, const FatTile& 
         uint8_t* A = lds + st * kABytes;
         uint8_t* B = lds + kStages * kABytes + st * kBBytes;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[r][jj];
+        for (int jj = 0; jj < NA; ++jj) *reinterpret_cast<v4u*>(A + swz(ar0 + 64 * jj, ac)) = ga[r][jj];
         decode_group_half<K, CB, 0>(gw[r], B, col0, 2 * tr);
         if (!helped) decode_group_half<K, CB, 1>(gw[r], B, col0, 2 * tr);
     };
@@ -908,7 +912,14 @@ __device__ __forceinline__ void fat_tile_k(const FatParams& p, const FatTile& ft
     // at most 128 rows: the second row half's MFMA waves help decode B
     const bool helped = ft.rows_valid <= 128 && fat_helpers_on(p);
     if (w % 3 == 0) {  // waves 0, 3, 6, 9: one per SIMD
-        fat_producer<CB, K>(p, ft, lds, nsteps, helped);
+        // the 64-row groups of A the consumers read: their fragments of
+        // rows, rounded up to 1, 2, 4, 6 or 8 per row half
+        if (ft.rows_valid <= 64)
+            fat_producer<CB, K, 1>(p, ft, lds, nsteps, helped);
+        else if (ft.rows_valid <= 128)
+            fat_producer<CB, K, 2>(p, ft, lds, nsteps, helped);
+        else
+            fat_producer<CB, K, 4>(p, ft, lds, nsteps, helped);
         return;
     }
     // consumers: c = 0..3 row half 0, 4..7 row half 1 (the helpers of a tile
