@@ -528,30 +528,52 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* y_
     for (int q = 0; q < kRowGroups; ++q)
 #pragma unroll
         for (int i = 0; i < 8; ++i) s[q][i] = 0.f;
-    for (int k = 0; k < topk; ++k) {
-        const int pos = route_pos[(int64_t)t * topk + k];
-        if (pos < 0) continue;  // wave-uniform
-        const uint16_t* sv = reinterpret_cast<const uint16_t*>(svh_d[row_expert[pos]]);
-        const int64_t wi = (int64_t)t * topk + k;
-        float w;
+    // the token's routes 64 at a time: lane k reads route k0 + k's sorted
+    // row, weight, expert and scale row (three dependent loads once per
+    // chunk, not per route); the routes then run in pairs, both rows' loads
+    // issued before the first butterfly, summed in route order
+    for (int k0 = 0; k0 < topk; k0 += 64) {
+        const int nk = min(64, topk - k0);
+        const int64_t wl = (int64_t)t * topk + k0 + min(lane, nk - 1);
+        const int my_pos = route_pos[wl];
+        float my_w;
         if (w_dtype == kF32)
-            w = reinterpret_cast<const float*>(weights)[wi];
+            my_w = reinterpret_cast<const float*>(weights)[wl];
         else if (w_dtype == kF16)
-            w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wi]);
+            my_w = (float)bits_to_half(reinterpret_cast<const uint16_t*>(weights)[wl]);
         else
-            w = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wi] << 16);
-        w *= had_sign(lane);  // had128_x8's lane sign
-        float v[kRowGroups][8], h[kRowGroups][8];
+            my_w = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(weights)[wl] << 16);
+        const int64_t my_sv = my_pos >= 0 ? svh_d[row_expert[my_pos]] : 0;
+        for (int k = 0; k < nk; k += 2) {
+            int pos[2];
+            const uint16_t* sv[2];
+            float w[2], v[2][kRowGroups][8], h[2][kRowGroups][8];
 #pragma unroll
-        for (int q = 0; q < kRowGroups; ++q) {
-            ld_f16x8(y_d, (int64_t)pos * H + rc.col[q], v[q]);
-            ld_f16x8(sv, rc.col[q], h[q]);
-        }
+            for (int u = 0; u < 2; ++u) {
+                const int ku = min(k + u, nk - 1);
+                pos[u] = k + u < nk ? __builtin_amdgcn_readlane(my_pos, ku) : -1;
+                sv[u] = reinterpret_cast<const uint16_t*>(
+                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_sv >> 32), ku) << 32) |
+                    (uint32_t)__builtin_amdgcn_readlane((int)my_sv, ku));
+                w[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), ku)) *
+                       had_sign(lane);  // had128_x8's lane sign
+                if (pos[u] < 0) continue;  // wave-uniform
 #pragma unroll
-        for (int q = 0; q < kRowGroups; ++q) {
-            had128_x8(v[q], lane);
+                for (int q = 0; q < kRowGroups; ++q) {
+                    ld_f16x8(y_d, (int64_t)pos[u] * H + rc.col[q], v[u][q]);
+                    ld_f16x8(sv[u], rc.col[q], h[u][q]);
+                }
+            }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s[q][i] += w * (v[q][i] * h[q][i]);
+            for (int u = 0; u < 2; ++u) {
+                if (pos[u] < 0) continue;
+#pragma unroll
+                for (int q = 0; q < kRowGroups; ++q) {
+                    had128_x8(v[u][q], lane);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) s[q][i] += w[u] * (v[u][q][i] * h[u][q][i]);
+                }
+            }
         }
     }
 #pragma unroll
