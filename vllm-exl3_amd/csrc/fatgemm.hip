@@ -724,8 +724,12 @@ __device__ __forceinline__ void load_group_words(uint32_t (&w)[K + 1], __amdgpu_
         w[2] = v[1];
         w[3] = v[2];
         w[4] = v[3];
-        if constexpr (K >= 5) w[5] = __builtin_amdgcn_raw_buffer_load_b32(trs, wfirst + 16, soff, 0);
-        if constexpr (K >= 6) w[6] = __builtin_amdgcn_raw_buffer_load_b32(trs, wfirst + 20, soff, 0);
+        if constexpr (K == 5) w[5] = __builtin_amdgcn_raw_buffer_load_b32(trs, wfirst + 16, soff, 0);
+        if constexpr (K == 6) {
+            const auto u = __builtin_amdgcn_raw_buffer_load_b64(trs, wfirst + 16, soff, 0);
+            w[5] = u[0];
+            w[6] = u[1];
+        }
     }
 }
 
