@@ -343,22 +343,22 @@ __global__ __launch_bounds__(256) void rotate_rows_kernel(RotateArgs a) {
     }
 }
 
-// Down-projection input rows, in image order: for every kept route, finish
-// gate/up (sum of the split partials, output rotation x svh, fp16 rounding,
-// activation, down suh, input rotation).  One wave per (route, 128-block of
-// the intermediate dimension); p carries the gate/up partials and tables.
-__global__ __launch_bounds__(256) void act_rows_kernel(GemvParams p, int n_routes, int topk,
-                                                       const int* route_pos, const int* row_expert,
-                                                       uint16_t* img) {
+// Down-projection input rows, in image order: for every sorted row (kept
+// route), finish gate/up (sum of the split partials, output rotation x svh,
+// fp16 rounding, activation, down suh, input rotation).  One wave per
+// (sorted row, 128-block of the intermediate dimension); p carries the
+// gate/up partials and tables.
+__global__ __launch_bounds__(256) void act_rows_kernel(GemvParams p, int n_rows, const int* n_sorted,
+                                                       const int* row_expert, uint16_t* img) {
     const int lane = threadIdx.x & 63;
     const int inter = p.in_features;
     const int nb = inter >> 7;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (unit >= (int64_t)n_routes * nb) return;
-    const int r = (int)(unit / nb), hb = (int)(unit % nb);
-    const int pos = route_pos[r];
-    if (pos < 0) return;  // wave-uniform
-    (void)topk;
+    if (unit >= (int64_t)n_rows * nb) return;
+    // sorted rows directly (rows past the kept routes exit): the partials
+    // and the row's expert are the first loads, no route lookup before them
+    const int pos = (int)(unit / nb), hb = (int)(unit % nb);
+    if (pos >= *n_sorted) return;  // wave-uniform
     const int e = row_expert[pos];
     Proj gu[2];
     gu[0].svh = reinterpret_cast<const uint16_t*>(p.tab[p.gateless ? 5 : 2][e]);
@@ -1744,7 +1744,7 @@ inline MoePlan plan_moe(int64_t T, int64_t topk, int64_t n_local, int64_t hidden
     m.dn = plan_phase((int)inter, (int)hidden, est_groups, m.max_groups, m.max_slots, m.MRB, true);
     size_t off = 0;
     m.off_route = off;
-    off += align256(sizeof(int) * (2 + 3 * (size_t)m.max_slots + 3 * (size_t)m.n_routes +
+    off += align256(sizeof(int) * (3 + 3 * (size_t)m.max_slots + 3 * (size_t)m.n_routes +
                                    3 * (size_t)m.max_groups));
     m.off_aux = off;  // sorted row -> route [routes]
     off += align256(sizeof(int) * (size_t)m.n_routes);
@@ -2149,6 +2149,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     ro.mt_slot = ro.n_mtiles + 1;
     ro.mt_row0 = ro.mt_slot + mp.max_groups;
     ro.mt_expert = ro.mt_row0 + mp.max_groups;
+    ro.n_sorted = ro.mt_expert + mp.max_groups;  // kept routes: the sorted rows act_rows_kernel walks
     const int64_t* tabs[9] = {gateless ? up_trellis : gate_trellis, gateless ? up_suh : gate_suh,
                               gateless ? up_svh : gate_svh, up_trellis, up_suh, up_svh,
                               down_trellis, down_suh, down_svh};
@@ -2308,8 +2309,8 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
     pd.x_stride = inter;
     profile_mark(3, st);
     const int64_t act_units = (int64_t)mp.n_routes * (inter / 128);
-    act_rows_kernel<<<(unsigned)((act_units + 3) / 4), 256, 0, st>>>(pd, mp.n_routes, (int)topk,
-                                                                     ro.route_pos, ro.row_expert, img_d);
+    act_rows_kernel<<<(unsigned)((act_units + 3) / 4), 256, 0, st>>>(pd, mp.n_routes, ro.n_sorted,
+                                                                     ro.row_expert, img_d);
     EXL3_LAUNCHED();
 
     // down: raw partials [S_d][routes][hidden]
