@@ -1144,15 +1144,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 // other value (csrc/p2b_moe.cu:295-324); this kernel does the same for the
 // units the streaming kernels skip, writing the same raw split partials, so
 // the consumer kernels need no change.  Workgroup = (slot, projection,
-// 128-column block); it exits at once for an expert of K 2..4 (the launch
-// costs a few microseconds when no such expert is routed) and otherwise
-// walks the splits and the slot's rows in groups of 16.  Per wave and tile
+// kAnyKBlocks 128-column blocks); it exits at once for an expert of K 2..4
+// (the launch costs a few microseconds when no such expert is routed) and
+// otherwise walks its column blocks, the splits and the slot's rows in
+// groups of 16.  Per wave and tile
 // row: the 256*K bytes are staged in the wave's LDS slot, each lane decodes
 // its four tile indices per tile with a general window read (any K), and
 // one v_mfma_f32_16x16x32_f16 per tile accumulates, in the operand order of
 // the streaming kernels (same image rows, same permuted tile positions).
 // ---------------------------------------------------------------------------
 constexpr int kAnyKMaxBytes = 256 * 8;  // one tile row at K <= 8
+// 128-column blocks per workgroup: in a phase with no K 5/6 expert every
+// workgroup only reads its slot's K and exits, so fewer, wider workgroups
+// cost less (C3: 8,224 -> 2,056 workgroups per gate/up launch).
+constexpr int kAnyKBlocks = 4;
 
 template <int CB, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv_anyk_kernel(GemvParams p) {
@@ -1162,10 +1167,11 @@ __global__ __launch_bounds__(kThreads) void gemv_anyk_kernel(GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nJB = p.out_features >> 7;
     const int nq = (MODE == kModeGateUp && !p.gateless) ? 2 : 1;
+    const int nJG = (nJB + kAnyKBlocks - 1) / kAnyKBlocks;
     const int item = blockIdx.x;
     const int qsel = item % nq;
-    const int jb = (item / nq) % nJB;
-    const int slot = item / nq / nJB;
+    const int jg = (item / nq) % nJG;
+    const int slot = item / nq / nJG;
     if (slot >= *p.n_active) return;
     const int e = p.slot_expert[slot];
     const bool up = MODE == kModeGateUp && (p.gateless || qsel);
@@ -1183,6 +1189,8 @@ __global__ __launch_bounds__(kThreads) void gemv_anyk_kernel(GemvParams p) {
     const int col_nu = sigma_col(lane & 15);
     const int q4 = 4 * lane_q(lane);
     uint8_t* st = stage_all[wave];
+    const int jb1 = min(nJB, (jg + 1) * kAnyKBlocks);
+    for (int jb = jg * kAnyKBlocks; jb < jb1; ++jb)
     for (int s = 0; s < p.S; ++s) {
         float* dst = p.ws + (((int64_t)qsel * p.S + s) * p.n_rows_ws + row_base) * p.out_features + jb * 128;
         // a halved-tail launch: slot 0 holds the whole input range, slot 1 zeros
@@ -1851,10 +1859,10 @@ hipError_t launch_gemv(int cb, int lk, const PhasePlan& ph, hipStream_t st, cons
 }
 
 // The units of a mixed-K MoE phase whose K is outside {2, 3, 4}: one
-// workgroup per (slot, streamed projection, 128-column block).
+// workgroup per (slot, streamed projection, kAnyKBlocks 128-column blocks).
 template <int MODE>
 hipError_t launch_anyk(int cb, int max_slots, int nq, hipStream_t st, const GemvParams& p) {
-    const int64_t grid = (int64_t)max_slots * nq * (p.out_features >> 7);
+    const int64_t grid = (int64_t)max_slots * nq * (((p.out_features >> 7) + kAnyKBlocks - 1) / kAnyKBlocks);
     if (grid < 1 || grid > 0x7FFFFFFF) return hipErrorInvalidValue;
     switch (cb) {
         case 0: gemv_anyk_kernel<0, MODE><<<(unsigned)grid, kThreads, 0, st>>>(p); break;
