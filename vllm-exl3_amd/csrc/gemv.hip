@@ -307,12 +307,16 @@ struct RotateArgs {
     int batch_m, n_ptr;
 };
 
+// BPW consecutive 128-input blocks of one row per wave: the row's metadata
+// loads (route position, expert, suh pointer) are paid once and the blocks'
+// activation and suh loads issue together.
+template <int BPW>
 __global__ __launch_bounds__(256) void rotate_rows_kernel(RotateArgs a) {
     const int lane = threadIdx.x & 63;
-    const int nb = a.in_f >> 7;
+    const int nb = a.in_f >> 7, nbw = (nb + BPW - 1) / BPW;
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (unit >= (int64_t)a.n_rows * nb) return;
-    const int r = (int)(unit / nb), hb = (int)(unit % nb);
+    if (unit >= (int64_t)a.n_rows * nbw) return;
+    const int r = (int)(unit / nbw), hb0 = (int)(unit % nbw) * BPW;
     int64_t row = r, tok = r;
     int e = 0;
     if (a.route_pos) {
@@ -326,20 +330,49 @@ __global__ __launch_bounds__(256) void rotate_rows_kernel(RotateArgs a) {
         if (e < 0 || e >= a.n_ptr) return;  // wave-uniform
         tok = r % a.batch_m;
     }
-    const int64_t fb = (int64_t)hb * 128;
-    const float x0 = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane);
-    const float x1 = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane + 64);
+    float x0[BPW], x1[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const int64_t fb = (int64_t)min(hb0 + i, nb - 1) * 128;  // a block past the row is not stored
+        x0[i] = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane);
+        x1[i] = load_act(a.x, a.x_dtype, tok * a.x_stride + fb + lane + 64);
+    }
+    const float hs = kHadNorm * had_sign64(lane);  // with had128's lane sign
     for (int q = 0; q < a.nproj; ++q) {
         const uint16_t* su = (a.route_pos || a.expert_list)
                                  ? reinterpret_cast<const uint16_t*>(a.suh_tab[q][e])
                                  : a.suh;
-        float v0 = x0 * (float)bits_to_half(su[fb + lane]);
-        float v1 = x1 * (float)bits_to_half(su[fb + lane + 64]);
-        had128(v0, v1, lane);
-        const float hs = kHadNorm * had_sign64(lane);  // with had128's lane sign
+        float v0[BPW], v1[BPW];
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) {
+            const int64_t fb = (int64_t)min(hb0 + i, nb - 1) * 128;
+            v0[i] = x0[i] * (float)bits_to_half(su[fb + lane]);
+            v1[i] = x1[i] * (float)bits_to_half(su[fb + lane + 64]);
+        }
         uint16_t* dst = a.img[q] + row * a.in_f;
-        dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0 * hs));
-        dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1 * hs));
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) {
+            if (hb0 + i >= nb) break;  // wave-uniform
+            const int64_t fb = (int64_t)(hb0 + i) * 128;
+            had128(v0[i], v1[i], lane);
+            dst[image_pos(fb + lane)] = half_to_bits(f32_to_f16_rne(v0[i] * hs));
+            dst[image_pos(fb + lane + 64)] = half_to_bits(f32_to_f16_rne(v1[i] * hs));
+        }
+    }
+}
+
+// Rotation launch: one wave per 128-input block while the grid fits about
+// one round of resident waves (32 per CU), else one wave per four blocks of
+// a row (the grid then still fills the chip; the per-wave load chain of the
+// row's metadata dominates such launches: C3, 27,648 one-block waves).
+inline void launch_rotate(const RotateArgs& ra, hipStream_t st) {
+    const int nb = ra.in_f >> 7;
+    const int64_t one = (int64_t)ra.n_rows * nb;
+    if (nb >= 4 && one > 32 * (int64_t)num_cus()) {
+        const int64_t units = (int64_t)ra.n_rows * ((nb + 3) / 4);
+        rotate_rows_kernel<4><<<(unsigned)((units + 3) / 4), 256, 0, st>>>(ra);
+    } else {
+        rotate_rows_kernel<1><<<(unsigned)((one + 3) / 4), 256, 0, st>>>(ra);
     }
 }
 
@@ -1964,8 +1997,7 @@ EXL3_API int exl3_linear(const void* x, int x_dtype, int64_t m, const int16_t* t
         p.x_dtype = x_dtype;
         p.x_raw = 1;
     } else {
-        const int64_t rot_units = m * (in_f / 128);
-        rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
+        launch_rotate(ra, st);
         EXL3_LAUNCHED();
     }
     profile_mark(1, st);
@@ -2075,8 +2107,7 @@ EXL3_API int exl3_gemv_batched(const void* x, int x_dtype, int64_t m, int64_t in
     p.n_rows_ws = (int)(n_sel * m);
     p.ws = reinterpret_cast<float*>(workspace);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const int64_t rot_units = n_sel * m * (in_features / 128);
-    rotate_rows_kernel<<<(unsigned)((rot_units + 3) / 4), 256, 0, st>>>(ra);
+    launch_rotate(ra, st);
     EXL3_LAUNCHED();
     EXL3_HIP(launch_gemv<kModeBatched>(codebook, (int)K, bp.ph, st, p));
     if (bp.ph.S > 1) {
@@ -2261,8 +2292,7 @@ EXL3_API int exl3_moe_forward(const void* x, int x_dtype, int64_t T, int64_t hid
         ra.nproj = mp.nproj;
         ra.img[0] = img_gu;
         ra.img[1] = img_gu1;
-        const int64_t gu_units = (int64_t)mp.n_routes * (hidden / 128);
-        rotate_rows_kernel<<<(unsigned)((gu_units + 3) / 4), 256, 0, st>>>(ra);
+        launch_rotate(ra, st);
         EXL3_LAUNCHED();
     }
 
